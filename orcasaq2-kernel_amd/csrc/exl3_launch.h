@@ -1,0 +1,42 @@
+// Host-side helpers shared by the kernel translation units: status codes and the
+// thread-local error message behind exl3_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/exl3hip.h"
+
+namespace exl3 {
+
+// Records a printf-style message for exl3_last_error() and returns `code`.
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Returns EXL3_OK, or records the pending launch error of `what`.
+int check_launch(const char* what);
+
+int reconstruct_dispatch(uint16_t* W, const uint32_t* trellis, int ic, int oc, int K, int cb,
+                         hipStream_t stream);
+int had_dispatch(const uint16_t* in, uint16_t* out, const uint16_t* pre, const uint16_t* post,
+                 float scale, long rows, int cols, hipStream_t stream);
+
+struct GemvShard {
+    const uint32_t* trellis;
+    const uint16_t* suh;
+    const uint16_t* svh;
+    uint16_t* C;       // (rows, ldc) fp16; this shard writes columns [0, oc)
+    int ic, oc, K, cb;
+    long ldc;
+};
+
+size_t gemv_workspace_bytes(int rows, int ic, int oc);
+int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows,
+                  void* workspace, size_t ws_bytes, hipStream_t stream);
+size_t gemm_workspace_bytes(int rows, int ic, int oc);
+int gemm_dispatch(const uint16_t* A, const uint32_t* trellis, uint16_t* C, const uint16_t* suh,
+                  const uint16_t* svh, void* workspace, size_t ws_bytes, int rows, int ic, int oc,
+                  int K, int cb, hipStream_t stream);
+int embed_dispatch(const int8_t* table, const void* scales, int scale_dtype, const int64_t* ids,
+                   void* out, long n_ids, int vocab, int dim, hipStream_t stream);
+
+}  // namespace exl3

@@ -1,0 +1,90 @@
+// Trellis reconstruct: packed tiles -> dense W_q (ic, oc) fp16, row-major.
+// Replaces exllamav3_ext.reconstruct as called at orcasaq2/ops.py:56 and
+// orcasaq2/__init__.py:57.  Output-write bound: 2 B/weight out against K/8 B in.
+//
+// One wave owns a strip of 8 tiles (tile row ti, tile columns 8g..8g+7): lane = 8T + c
+// decodes chunk c of tile T, the decoded 16x128 block is staged in LDS, and the wave
+// writes it back as 16-byte stores that cover whole 256-byte row segments.
+#include "exl3_common.h"
+#include "exl3_launch.h"
+
+namespace exl3 {
+
+constexpr int RC_WAVES = 4;
+constexpr int RC_STRIDE = 128 + 8;  // halves per staged row (padding against bank conflicts)
+
+template <int K, int CB>
+__global__ __launch_bounds__(64 * RC_WAVES) void reconstruct_kernel(
+    uint16_t* __restrict__ W, const uint32_t* __restrict__ trellis, int ic, int oc)
+{
+    __shared__ uint16_t stage[RC_WAVES][16 * RC_STRIDE];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int tc = oc >> 4;
+    const int groups = (tc + 7) >> 3;
+    const long task = (long)blockIdx.x * RC_WAVES + wave;
+    const bool active = task < (long)(ic >> 4) * groups;
+    const int ti = active ? (int)(task / groups) : 0, g = active ? (int)(task % groups) : 0;
+    const int T = lane >> 3, c = lane & 7;
+    const int tn = g * 8 + T;
+    uint16_t* st = stage[wave];
+
+    if (active && tn < tc) {
+        const uint32_t* tile = trellis + ((long)ti * tc + tn) * (8 * K);
+        uint32_t w[K + 1];
+        load_chunk<K>(w, tile, c);
+        // position q = 8m + i -> row 2m + {0,1,8,9}[i%4], column c + 8(i/4)
+#define EXL3_RC(Q)                                                                         \
+    {                                                                                      \
+        constexpr int m = (Q) / 8, i = (Q) % 8;                                            \
+        constexpr int row = 2 * m + ((i & 3) == 0 ? 0 : (i & 3) == 1 ? 1 : (i & 3) == 2 ? 8 : 9); \
+        constexpr int col8 = 8 * (i >> 2);                                                 \
+        _Float16 v = cb_value<CB>(chunk_state<K, (Q)>(w));                                 \
+        st[row * RC_STRIDE + 16 * T + c + col8] = __builtin_bit_cast(uint16_t, v);        \
+    }
+        EXL3_RC(0) EXL3_RC(1) EXL3_RC(2) EXL3_RC(3) EXL3_RC(4) EXL3_RC(5) EXL3_RC(6) EXL3_RC(7)
+        EXL3_RC(8) EXL3_RC(9) EXL3_RC(10) EXL3_RC(11) EXL3_RC(12) EXL3_RC(13) EXL3_RC(14) EXL3_RC(15)
+        EXL3_RC(16) EXL3_RC(17) EXL3_RC(18) EXL3_RC(19) EXL3_RC(20) EXL3_RC(21) EXL3_RC(22) EXL3_RC(23)
+        EXL3_RC(24) EXL3_RC(25) EXL3_RC(26) EXL3_RC(27) EXL3_RC(28) EXL3_RC(29) EXL3_RC(30) EXL3_RC(31)
+#undef EXL3_RC
+    }
+    __syncthreads();
+
+    // 16 rows x 256 bytes: each store instruction covers 4 rows, 16 bytes per lane.
+    const int seg = lane & 15;          // 16-byte segment within the row (8 halves)
+    const int col0 = g * 128 + seg * 8;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const int row = s * 4 + (lane >> 4);
+        if (active && col0 < oc) {
+            const uint4 v = *reinterpret_cast<const uint4*>(st + row * RC_STRIDE + seg * 8);
+            *reinterpret_cast<uint4*>(W + (long)(ti * 16 + row) * oc + col0) = v;
+        }
+    }
+}
+
+template <int K, int CB>
+static int launch_reconstruct(uint16_t* W, const uint32_t* trellis, int ic, int oc, hipStream_t stream)
+{
+    const long tasks = (long)(ic / 16) * ((oc / 16 + 7) / 8);
+    const long blocks = (tasks + RC_WAVES - 1) / RC_WAVES;
+    hipLaunchKernelGGL((reconstruct_kernel<K, CB>), dim3((unsigned)blocks), dim3(64 * RC_WAVES), 0,
+                       stream, W, trellis, ic, oc);
+    return check_launch("exl3_reconstruct");
+}
+
+int reconstruct_dispatch(uint16_t* W, const uint32_t* trellis, int ic, int oc, int K, int cb,
+                         hipStream_t stream)
+{
+#define EXL3_CASE(KK)                                                                          \
+    case KK:                                                                                   \
+        return cb == CB_MCG ? launch_reconstruct<KK, CB_MCG>(W, trellis, ic, oc, stream)       \
+                            : launch_reconstruct<KK, CB_3INST>(W, trellis, ic, oc, stream);
+    switch (K) {
+        EXL3_CASE(1) EXL3_CASE(2) EXL3_CASE(3) EXL3_CASE(4)
+        EXL3_CASE(5) EXL3_CASE(6) EXL3_CASE(7) EXL3_CASE(8)
+    }
+#undef EXL3_CASE
+    return set_error(EXL3_ERR_ARG, "exl3_reconstruct: K=%d is not in 1..8", K);
+}
+
+}  // namespace exl3

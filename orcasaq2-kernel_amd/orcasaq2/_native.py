@@ -1,0 +1,288 @@
+"""ctypes binding of libexl3hip.so (include/exl3hip.h) for torch tensors on the GPU.
+
+This is the only place Python crosses into native code.  Each wrapper validates device,
+dtype, contiguity and shapes on the host (raising RuntimeError, as the reference's
+extension does, e.g. orcasaq2/ops.py:29-31), allocates outputs and workspaces through
+torch's caching allocator, and enqueues on torch's current stream.  There is no fallback:
+if the library is missing or a tensor is not on the GPU, the call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+LIB_NAME = "libexl3hip.so"
+LIB_PATH = os.environ.get("ORCASAQ2_LIB", os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME))
+ABI_VERSION = 1
+
+CB_3INST, CB_MCG, CB_MUL1 = 0, 1, 2
+GEMV_MAX_ROWS = 16
+MAX_SHARDS = 64
+
+_lib = None
+_lock = threading.Lock()
+
+
+class Shard(ctypes.Structure):
+    """exl3_shard_t."""
+    _fields_ = [("trellis", ctypes.c_void_p), ("suh", ctypes.c_void_p), ("svh", ctypes.c_void_p),
+                ("C", ctypes.c_void_p), ("ldc", ctypes.c_long), ("oc", ctypes.c_int),
+                ("K", ctypes.c_int), ("codebook", ctypes.c_int)]
+
+
+_SIGS = {
+    "exl3_last_error": (ctypes.c_char_p, []),
+    "exl3_abi_version": (ctypes.c_int, []),
+    "exl3_reconstruct": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "exl3_had_r_128": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_float, ctypes.c_long, ctypes.c_int, ctypes.c_void_p]),
+    "exl3_gemv_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "exl3_gemv": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                 ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "exl3_gemv_grouped_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Shard), ctypes.c_int,
+                                                            ctypes.c_int, ctypes.c_int]),
+    "exl3_gemv_grouped": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Shard), ctypes.c_int,
+                                         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_void_p]),
+    "exl3_gemm_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "exl3_gemm": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                 ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "exl3_embed_int8_gather": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                              ctypes.c_void_p, ctypes.c_void_p, ctypes.c_long,
+                                              ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+}
+
+EXPORTED = tuple(_SIGS)
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libexl3hip.so (after torch, so the HIP runtime torch mapped is reused)."""
+    global _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(
+                    f"orcasaq2 needs its HIP library and {LIB_PATH} does not exist. Build it with\n"
+                    "  python orcasaq2-kernel_amd/build_lib.py\n"
+                    "(hipcc --offload-arch=gfx950; cross-compiles without a GPU).")
+            L = ctypes.CDLL(LIB_PATH)
+            for name, (res, args) in _SIGS.items():
+                fn = getattr(L, name)
+                fn.restype = res
+                fn.argtypes = args
+            v = L.exl3_abi_version()
+            if v != ABI_VERSION:
+                raise RuntimeError(f"orcasaq2: {LIB_PATH} has ABI {v}, this package wants {ABI_VERSION}")
+            _lib = L
+    return _lib
+
+
+def _check(rc: int, fn: str) -> None:
+    if rc != 0:
+        msg = lib().exl3_last_error().decode(errors="replace")
+        raise RuntimeError(f"{fn} failed ({rc}): {msg}")
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _need_gpu(fn: str, *ts: torch.Tensor) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(f"{fn}: tensors must be on the GPU (got {t.device}); "
+                               "orcasaq2 has no CPU path")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"{fn}: tensors on different devices ({dev} and {t.device})")
+    return dev
+
+
+def _need(cond: bool, fn: str, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(f"{fn}: {msg}")
+
+
+def codebook_id(mcg: bool, mul1: bool) -> int:
+    if mul1:
+        raise RuntimeError("orcasaq2: the mul1 codebook is not supported by the HIP kernels")
+    return CB_MCG if mcg else CB_3INST
+
+
+def check_trellis(fn: str, trellis: torch.Tensor, ic: int, oc: int, K) -> int:
+    """trellis must be int16 (ic/16, oc/16, 16K), contiguous (orcasaq2/ops.py:28-34)."""
+    _need(trellis.dtype in (torch.int16, torch.uint16), fn, f"trellis must be int16, got {trellis.dtype}")
+    _need(trellis.is_contiguous(), fn, "trellis must be contiguous")
+    if not float(K).is_integer():
+        raise RuntimeError(f"{fn}: K={K}: half-rate (mul1) trellis widths are not supported")
+    K = int(K)
+    _need(1 <= K <= 8, fn, f"K={K} is not in 1..8")
+    _need(trellis.dim() == 3 and trellis.shape[0] * 16 == ic and trellis.shape[1] * 16 == oc, fn,
+          f"trellis shape {tuple(trellis.shape)} does not match ic={ic}, oc={oc}")
+    _need(trellis.shape[2] == 16 * K, fn, f"packed dimension 2 is incorrect size "
+          f"({trellis.shape[2]} for K={K})")
+    return K
+
+
+def _vec16(fn: str, name: str, t: torch.Tensor, n: int) -> None:
+    _need(t.dtype == torch.float16, fn, f"{name} must be fp16, got {t.dtype}")
+    _need(t.is_contiguous() and t.numel() == n, fn, f"{name} must be contiguous with {n} elements")
+
+
+# ---------------------------------------------------------------- workspaces
+
+_ws: dict[tuple, torch.Tensor] = {}
+
+
+def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-initialised GEMV workspace, one per (device, stream).  The kernels leave its
+    ticket counters at zero, so it is reused by every later call on that stream."""
+    stream = torch.cuda.current_stream(device)
+    key = (device.index, stream.cuda_stream)
+    ws = _ws.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _ws[key] = ws
+    return ws
+
+
+# ---------------------------------------------------------------- entry points
+
+def reconstruct(trellis: torch.Tensor, K, codebook: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """W_q (ic, oc) fp16 from trellis (ic/16, oc/16, 16K) -- ext.reconstruct (orcasaq2/ops.py:56)."""
+    fn = "exl3_reconstruct"
+    dev = _need_gpu(fn, trellis, out)
+    ic, oc = trellis.shape[0] * 16, trellis.shape[1] * 16
+    K = check_trellis(fn, trellis, ic, oc, K)
+    if out is None:
+        out = torch.empty((ic, oc), dtype=torch.float16, device=dev)
+    _need(out.dtype == torch.float16 and out.is_contiguous() and tuple(out.shape) == (ic, oc), fn,
+          "out must be contiguous fp16 (ic, oc)")
+    _check(lib().exl3_reconstruct(_ptr(out), _ptr(trellis), ic, oc, K, codebook, _stream(dev)), fn)
+    return out
+
+
+def had_r_128(x: torch.Tensor, out: torch.Tensor | None = None, pre: torch.Tensor | None = None,
+              post: torch.Tensor | None = None, scale: float = 1.0) -> torch.Tensor:
+    """Row-wise block-128 Hadamard with optional pre/post scales -- ext.had_r_128
+    (orcasaq2/ops.py:54, 59).  out may be x (in place)."""
+    fn = "exl3_had_r_128"
+    dev = _need_gpu(fn, x, out, pre, post)
+    _need(x.dtype == torch.float16 and x.is_contiguous(), fn, "x must be contiguous fp16")
+    cols = x.shape[-1]
+    _need(cols % 128 == 0, fn, f"last dim {cols} is not a multiple of 128")
+    rows = x.numel() // cols if cols else 0
+    if out is None:
+        out = torch.empty_like(x)
+    _need(out.dtype == torch.float16 and out.is_contiguous() and out.shape == x.shape, fn,
+          "out must match x")
+    for name, v in (("pre", pre), ("post", post)):
+        if v is not None:
+            _vec16(fn, name, v, cols)
+    _check(lib().exl3_had_r_128(_ptr(x), _ptr(out), _ptr(pre), _ptr(post), float(scale), rows, cols,
+                                _stream(dev)), fn)
+    return out
+
+
+def gemv_grouped(x: torch.Tensor, shards: list[dict], out: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused decode-GEMV of 1..16 rows through one or more shards that share x; returns
+    (rows, sum oc) with the shards' outputs side by side (the concat of
+    orcasaq2/config.py:243 written in place).  Each shard: dict(trellis, suh, svh, oc, K,
+    codebook)."""
+    fn = "exl3_gemv"
+    _need(x.dim() == 2, fn, "x must be (rows, ic)")
+    rows, ic = x.shape
+    dev = _need_gpu(fn, x, out, *[s["trellis"] for s in shards])
+    _need(x.dtype == torch.float16 and x.is_contiguous(), fn, "x must be contiguous fp16")
+    _need(1 <= rows <= GEMV_MAX_ROWS, fn, f"rows={rows} is not in 1..{GEMV_MAX_ROWS}")
+    _need(1 <= len(shards) <= MAX_SHARDS, fn, f"{len(shards)} shards")
+    total = sum(int(s["oc"]) for s in shards)
+    if out is None:
+        out = torch.empty((rows, total), dtype=torch.float16, device=dev)
+    _need(out.dtype == torch.float16 and out.is_contiguous() and tuple(out.shape) == (rows, total), fn,
+          f"out must be contiguous fp16 ({rows}, {total})")
+    arr = (Shard * len(shards))()
+    col = 0
+    for i, s in enumerate(shards):
+        oc = int(s["oc"])
+        K = check_trellis(fn, s["trellis"], ic, oc, s["K"])
+        _vec16(fn, "suh", s["suh"], ic)
+        _vec16(fn, "svh", s["svh"], oc)
+        arr[i] = Shard(s["trellis"].data_ptr(), s["suh"].data_ptr(), s["svh"].data_ptr(),
+                       out.data_ptr() + 2 * col, total, oc, K, int(s["codebook"]))
+        col += oc
+    L = lib()
+    nbytes = L.exl3_gemv_grouped_workspace_bytes(arr, len(shards), rows, ic)
+    ws = gemv_workspace(dev, nbytes)
+    _check(L.exl3_gemv_grouped(_ptr(x), arr, len(shards), _ptr(ws), ws.numel(), rows, ic, _stream(dev)), fn)
+    return out
+
+
+def gemv(x, trellis, suh, svh, K, codebook, out=None) -> torch.Tensor:
+    """ext.exl3_gemm for rows <= 16 (orcasaq2/ops.py:46-49)."""
+    oc = svh.numel()
+    return gemv_grouped(x, [dict(trellis=trellis, suh=suh, svh=svh, oc=oc, K=K, codebook=codebook)], out)
+
+
+def gemm(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, K, codebook: int,
+         out: torch.Tensor | None = None) -> torch.Tensor:
+    """Prefill path: Hadamard of x into a scratch, fused decode-into-MFMA GEMM with the
+    output Hadamard in its epilogue (replaces orcasaq2/ops.py:50-59)."""
+    fn = "exl3_gemm"
+    _need(x.dim() == 2, fn, "x must be (rows, ic)")
+    rows, ic = x.shape
+    oc = svh.numel()
+    dev = _need_gpu(fn, x, trellis, suh, svh, out)
+    _need(x.dtype == torch.float16 and x.is_contiguous(), fn, "x must be contiguous fp16")
+    K = check_trellis(fn, trellis, ic, oc, K)
+    _vec16(fn, "suh", suh, ic)
+    _vec16(fn, "svh", svh, oc)
+    if out is None:
+        out = torch.empty((rows, oc), dtype=torch.float16, device=dev)
+    _need(out.dtype == torch.float16 and out.is_contiguous() and tuple(out.shape) == (rows, oc), fn,
+          "out must be contiguous fp16 (rows, oc)")
+    if rows == 0:
+        return out
+    L = lib()
+    nbytes = L.exl3_gemm_workspace_bytes(rows, ic, oc)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    _check(L.exl3_gemm(_ptr(x), _ptr(trellis), _ptr(out), _ptr(suh), _ptr(svh), _ptr(ws), nbytes, rows, ic,
+                       oc, K, codebook, _stream(dev)), fn)
+    return out
+
+
+_SCALE_DTYPES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def embed_int8(table: torch.Tensor, scales: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+    """table[ids].to(scales.dtype) * scales[ids] (orcasaq2/heads.py:66-67); output shape
+    ids.shape + (dim,)."""
+    fn = "exl3_embed_int8_gather"
+    dev = _need_gpu(fn, table, scales, ids)
+    _need(table.dtype == torch.int8 and table.dim() == 2 and table.is_contiguous(), fn,
+          "table must be contiguous int8 (vocab, dim)")
+    vocab, dim = table.shape
+    _need(dim % 4 == 0, fn, f"dim={dim} must be a multiple of 4")
+    _need(scales.dtype in _SCALE_DTYPES, fn, f"scales dtype {scales.dtype}")
+    _need(scales.is_contiguous() and scales.numel() == vocab, fn, "scales must be contiguous (vocab) or (vocab, 1)")
+    idx = ids.reshape(-1)
+    if idx.dtype != torch.int64 or not idx.is_contiguous():
+        idx = idx.to(torch.int64).contiguous()
+    out = torch.empty((idx.numel(), dim), dtype=scales.dtype, device=dev)
+    _check(lib().exl3_embed_int8_gather(_ptr(table), _ptr(scales), _SCALE_DTYPES[scales.dtype], _ptr(idx),
+                                        _ptr(out), idx.numel(), vocab, dim, _stream(dev)), fn)
+    return out.reshape(*ids.shape, dim)

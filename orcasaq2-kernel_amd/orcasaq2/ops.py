@@ -1,0 +1,85 @@
+"""The EXL3 shard GEMM as PyTorch custom ops (same names and schema as the reference's
+orcasaq2/ops.py:37-66), backed by the gfx950 HIP library through its C ABI.
+
+A custom op keeps the shard opaque to Dynamo -- one graph node with a known output shape
+(the register_fake below) -- so a torch.compile'd model compiles around it, and its
+kernels only enqueue on the current stream, so it can be captured in a HIP graph.
+
+Dispatch on the number of activation rows (reference: orcasaq2/ops.py:25, 46-59):
+  * rows <= 16            fused decode-GEMV (exl3_gemv): packed words streamed from HBM,
+                          decoded in registers, MFMA accumulate, split-K, output Hadamard;
+  * 16 < rows <= GEMM_MAX_ROWS
+                          fused decode-GEMM (exl3_gemm): Hadamard pass over x, then tiles
+                          decoded straight into MFMA operands, output Hadamard in the epilogue;
+  * rows > GEMM_MAX_ROWS  the reference's reconstruct branch: had_r_128(x, suh), dense W_q
+                          into a scratch freed on exit, library fp16 GEMM, had_r_128(y, svh).
+The op is registered for the "cuda" device type (ROCm) only: there is no CPU path.
+"""
+
+import os
+
+import torch
+from torch import Tensor
+
+from . import _native
+
+# Rows at or below which the fused kernels are used (the reference's default and env knob,
+# orcasaq2/ops.py:22-25).  Above it the dense W_q is rebuilt once and a library GEMM runs.
+GEMM_MAX_ROWS = int(os.environ.get("ORCA_EXL3_GEMM_MAX_ROWS", "144"))
+GEMV_MAX_ROWS = _native.GEMV_MAX_ROWS
+
+
+def exl3_K(trellis: Tensor):
+    """Bits per weight = trellis.shape[-1] / 16 (16-weight steps per tile row).  Integers
+    stay int; the mul1 half rates (1.5/2.5/3.5: 24/40/56 words per tile) stay float, as in
+    orcasaq2/ops.py:28-34.  The HIP kernels accept integer K in 1..8 only."""
+    k = trellis.shape[-1] / 16
+    return int(k) if float(k).is_integer() else k
+
+
+def _shard_gemm_impl(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, oc: int, k: float,
+                     mcg: bool, mul1: bool) -> Tensor:
+    cb = _native.codebook_id(mcg, mul1)
+    if float(k).is_integer():
+        k = int(k)
+    rows, ic = x.shape
+    if rows == 0:
+        return x.new_empty((0, oc), dtype=torch.half)
+    if rows <= GEMV_MAX_ROWS:
+        return _native.gemv(x, trellis, suh, svh, k, cb)
+    if rows <= GEMM_MAX_ROWS:
+        return _native.gemm(x, trellis, suh, svh, k, cb)
+    # reconstruct branch: dense W_q lives only for the duration of the call
+    xh = _native.had_r_128(x, pre=suh)
+    w = _native.reconstruct(trellis, k, cb)
+    y = torch.matmul(xh, w)
+    del w, xh
+    return _native.had_r_128(y, out=y, post=svh)
+
+
+@torch.library.custom_op("orcasaq2::shard_gemm", mutates_args=(), device_types="cuda")
+def shard_gemm(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor,
+               oc: int, k: float, mcg: bool, mul1: bool) -> Tensor:
+    return _shard_gemm_impl(x, trellis, suh, svh, oc, k, mcg, mul1)
+
+
+@shard_gemm.register_fake
+def _shard_gemm_fake(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor,
+                     oc: int, k: float, mcg: bool, mul1: bool) -> Tensor:
+    return x.new_empty((x.shape[0], oc), dtype=torch.half)
+
+
+@torch.library.custom_op("orcasaq2::shards_gemv", mutates_args=(), device_types="cuda")
+def shards_gemv(x: Tensor, trellis: list[Tensor], suh: list[Tensor], svh: list[Tensor],
+                oc: list[int], k: list[float], mcg: list[bool], mul1: list[bool]) -> Tensor:
+    """All shards of a fused layer (q/k/v, gate/up) for rows <= 16 in as few launches as
+    there are distinct (K, codebook); outputs are written side by side, which is the
+    per-shard loop + torch.cat of orcasaq2/config.py:237-243 without the copy."""
+    shards = [dict(trellis=t, suh=a, svh=b, oc=o, K=kk, codebook=_native.codebook_id(m, m1))
+              for t, a, b, o, kk, m, m1 in zip(trellis, suh, svh, oc, k, mcg, mul1)]
+    return _native.gemv_grouped(x, shards)
+
+
+@shards_gemv.register_fake
+def _shards_gemv_fake(x, trellis, suh, svh, oc, k, mcg, mul1) -> Tensor:
+    return x.new_empty((x.shape[0], sum(oc)), dtype=torch.half)

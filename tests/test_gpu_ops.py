@@ -1,0 +1,157 @@
+"""GPU tests of the drop-in surface: the orcasaq2::shard_gemm / shards_gemv custom ops
+(all three row branches), HIP-graph capture and replay, torch.compile around the op,
+and Exl3LinearMethod.apply through a stand-in vLLM layer."""
+import numpy as np
+import pytest
+import torch
+
+import orcasaq2  # noqa: F401
+from orcasaq2 import ops as O
+from orcasaq2 import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+D = torch.device("cuda", 0)
+
+
+def on(lin):
+    return {k: (v.to(D) if isinstance(v, torch.Tensor) else v) for k, v in lin.items()}
+
+
+def ref(oracle, x, lin, cb=0):
+    return oracle.shard_gemm_ref(x.cpu().numpy(), lin["trellis"], lin["suh"].numpy(), lin["svh"].numpy(),
+                                 lin["K"], cb)
+
+
+@pytest.mark.parametrize("rows", [1, 16, 17, 144, 145, 400])
+def test_shard_gemm_branches(native, oracle, rows):
+    lin = syn.linear(512, 256, 4, seed=rows)
+    x = syn.activations(rows, 512, torch.Generator().manual_seed(rows))
+    d = on(lin)
+    y = torch.ops.orcasaq2.shard_gemm(x.to(D), d["trellis"], d["suh"], d["svh"], 256, 4.0, False, False)
+    assert y.dtype == torch.half and y.shape == (rows, 256)
+    assert oracle.rel_err_rows(y.cpu().numpy(), ref(oracle, x, lin)).max() <= 1e-3
+
+
+def test_shard_gemm_rejects_mul1_and_half_rates(native):
+    lin = on(syn.linear(256, 256, 4, seed=1))
+    x = torch.zeros(1, 256, dtype=torch.half, device=D)
+    with pytest.raises(RuntimeError, match="mul1"):
+        torch.ops.orcasaq2.shard_gemm(x, lin["trellis"], lin["suh"], lin["svh"], 256, 4.0, False, True)
+    bad = torch.zeros(16, 16, 56, dtype=torch.int16, device=D)
+    with pytest.raises(RuntimeError, match="half-rate|packed dimension"):
+        torch.ops.orcasaq2.shard_gemm(x, bad, lin["suh"], lin["svh"], 256, 3.5, False, False)
+
+
+def test_shard_gemm_wrong_width_message(native):
+    lin = on(syn.linear(256, 256, 4, seed=1))
+    x = torch.zeros(1, 256, dtype=torch.half, device=D)
+    with pytest.raises(RuntimeError, match="packed dimension 2 is incorrect size"):
+        torch.ops.orcasaq2.shard_gemm(x, lin["trellis"], lin["suh"], lin["svh"], 256, 3.0, False, False)
+
+
+def test_hip_graph_capture_replays(native, oracle):
+    lins = [syn.linear(1024, oc, K, seed=i) for i, (oc, K) in enumerate([(512, 4), (256, 5)])]
+    ds = [on(l) for l in lins]
+    x = syn.activations(2, 1024, torch.Generator().manual_seed(1)).to(D)
+
+    def step():
+        a = torch.ops.orcasaq2.shard_gemm(x, ds[0]["trellis"], ds[0]["suh"], ds[0]["svh"], 512, 4.0, False, False)
+        b = torch.ops.orcasaq2.shards_gemv(x, [d["trellis"] for d in ds], [d["suh"] for d in ds],
+                                           [d["svh"] for d in ds], [512, 256], [4.0, 5.0], [False, False],
+                                           [False, False])
+        return a, b
+
+    eager = step()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()  # warm the per-stream workspace outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = step()
+    for i in range(4):
+        x.copy_(syn.activations(2, 1024, torch.Generator().manual_seed(1)).to(D))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out[0], eager[0]) and torch.equal(out[1], eager[1]), i
+        step()  # eager work between replays
+        torch.cuda.synchronize()
+
+
+def test_torch_compile_treats_op_as_opaque(native):
+    lin = on(syn.linear(256, 256, 3, seed=4))
+    x = syn.activations(1, 256, torch.Generator().manual_seed(4)).to(D)
+
+    def f(x):
+        y = torch.ops.orcasaq2.shard_gemm(x * 1.0, lin["trellis"], lin["suh"], lin["svh"], 256, 3.0, False, False)
+        return y.float().sum(-1)
+
+    want = f(x)
+    got = torch.compile(f, backend="eager", fullgraph=True)(x)
+    assert torch.equal(want, got)
+
+
+def test_linear_method_apply_fused_layers(native, oracle):
+    """qkv_proj-style layer: shards captured by slot, processed, applied (grouped op at
+    <= 16 rows, per-shard ops + cat above), bias added, dtype restored."""
+    from orcasaq2.config import Exl3Config, Exl3LinearMethod
+    from orcasaq2._vllm_compat import LinearBase
+    cfg = Exl3Config.from_config({"bits": 4})
+    spec = [("q", 512, 4), ("k", 128, 5), ("v", 128, 5)]
+    lins = {sid: syn.linear(256, oc, K, seed=i) for i, (sid, oc, K) in enumerate(spec)}
+    layer = LinearBase(256, 768, bias=True, params_dtype=torch.bfloat16, quant_config=cfg,
+                       prefix="model.layers.0.self_attn.qkv_proj", output_partition_sizes=[512, 128, 128])
+    assert isinstance(layer.quant_method, Exl3LinearMethod)
+    for sid in ("v", "q", "k"):  # arrival order must not matter
+        for name in ("trellis", "suh", "svh"):
+            p = getattr(layer, name)
+            p.weight_loader(p, lins[sid][name].to(D), sid)
+    layer.bias.data = torch.randn(768).to(torch.bfloat16)
+    layer.quant_method.process_weights_after_loading(layer)
+    layer.bias.data = layer.bias.data.to(D)
+    for rows in (1, 5, 40):
+        x = syn.activations(rows, 256, torch.Generator().manual_seed(rows)).to(torch.bfloat16)
+        y = layer(x.to(D))
+        assert y.dtype == torch.bfloat16 and y.shape == (rows, 768)
+        xh = x.half()
+        col = 0
+        for sid, oc, K in spec:
+            want = ref(oracle, xh, lins[sid]) + layer.bias.float().cpu().numpy()[col:col + oc]
+            got = y[:, col:col + oc].float().cpu().numpy()
+            err = np.linalg.norm(got - want, axis=1) / np.linalg.norm(want, axis=1)
+            assert err.max() < 1e-2, (sid, rows, err.max())  # bf16 output rounding
+            col += oc
+
+
+def test_embedding_method_int8_on_gpu(native):
+    from orcasaq2.config import Exl3Config
+    from orcasaq2._vllm_compat import VocabParallelEmbedding
+    cfg = Exl3Config.from_config({})
+    emb = VocabParallelEmbedding(1000, 64, params_dtype=torch.bfloat16, quant_config=cfg)
+    g = torch.Generator().manual_seed(3)
+    q = torch.randint(-128, 128, (1000, 64), generator=g, dtype=torch.int8)
+    s = torch.rand(1000, generator=g) * 0.01
+    emb.qweight.weight_loader(emb.qweight, q.to(D))
+    emb.scales.weight_loader(emb.scales, s.to(D))
+    emb.quant_method.process_weights_after_loading(emb)
+    ids = torch.tensor([3, 999, 0, 3], device=D)
+    out = emb(ids)
+    want = q[ids.cpu()].to(torch.bfloat16) * s.to(torch.bfloat16).reshape(-1, 1)[ids.cpu()]
+    assert torch.equal(out.cpu(), want)
+
+
+def test_reconstruct_weight_dense_equivalence(native, oracle):
+    """F.linear(x, reconstruct_weight(...)) matches the fused op (orcasaq2/__init__.py:49-61
+    against orcasaq2/ops.py:53-59)."""
+    from orcasaq2 import reconstruct_weight
+    lin = syn.linear(256, 384, 4, seed=12)
+    d = on(lin)
+    W = reconstruct_weight(d["trellis"], d["suh"], d["svh"], None, None)
+    assert W.shape == (384, 256) and W.dtype == torch.half
+    x = syn.activations(3, 256, torch.Generator().manual_seed(12)).to(D)
+    y_dense = torch.nn.functional.linear(x.float(), W.float())
+    y = torch.ops.orcasaq2.shard_gemm(x, d["trellis"], d["suh"], d["svh"], 384, 4.0, False, False)
+    err = torch.linalg.norm(y.float() - y_dense, dim=1) / torch.linalg.norm(y_dense, dim=1)
+    assert err.max().item() < 2e-3
