@@ -17,10 +17,9 @@
  *   - codebook: EXL3_CB_3INST (neither .mcg nor .mul1 tensor present), EXL3_CB_MCG
  *     (.mcg present) -- the flags of orcasaq2/config.py:218.  EXL3_CB_MUL1 is reported
  *     as EXL3_ERR_UNSUPPORTED.
- *   - Workspaces are caller-owned device buffers of at least the *_workspace_bytes()
- *     size.  The GEMV workspace must be zero-filled before its first use; every GEMV call
- *     leaves its ticket counters at zero again, so a workspace can be reused by later
- *     calls ordered on one stream (calls that overlap in time must not share one).
+ *   - Workspaces are caller-owned device buffers (256-byte aligned) of at least the
+ *     *_workspace_bytes() size, with no required contents; a call uses its workspace until
+ *     its last kernel has run, so calls that may overlap in time must not share one.
  */
 #ifndef EXL3HIP_H
 #define EXL3HIP_H

@@ -32,56 +32,10 @@ enum Codebook : int { CB_3INST = 0, CB_MCG = 1, CB_MUL1 = 2 };
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// ---------------------------------------------------------------- codebook
-
-// Masked codebook word: two fp16 halves whose sum is the weight.
-template <int CB>
-__device__ __forceinline__ uint32_t cb_word(uint32_t s)
-{
-    uint32_t x;
-    if constexpr (CB == CB_MCG) {
-        x = s * 0xCBAC1FEDu;
-    } else {
-        // (a*s + b) mod 2^32 with s < 2^16: a = 1361*2^16 + 31858, b = 64248484.
-        // t = 31858*s + b fits a 16x16+32 multiply-add; the high half gets 1361*s.
-        uint32_t t = (s & 0xffffu) * 31858u + 64248484u;
-        x = t + ((s * 1361u) << 16);
-    }
-    return (x & 0x8FFF8FFFu) ^ 0x3B603B60u;
-}
-
-__device__ __forceinline__ _Float16 half_sum(uint32_t x)
-{
-    _Float16 lo = __builtin_bit_cast(_Float16, (uint16_t)(x & 0xffffu));
-    _Float16 hi = __builtin_bit_cast(_Float16, (uint16_t)(x >> 16));
-    return lo + hi;
-}
-
-template <int CB>
-__device__ __forceinline__ _Float16 cb_value(uint32_t s)
-{
-    return half_sum(cb_word<CB>(s));
-}
-
 // ---------------------------------------------------------------- stream access
 
-// w[0] = the u32 word preceding the chunk (wrapping within the tile), w[1..K] = the
-// chunk's K words.  State of chunk position q (compile-time): the low 16 bits of the
-// 32-bit window ending at bit 32 + (q+1)K of the concatenation w[0]:w[1]:...:w[K].
-template <int K, int Q>
-__device__ __forceinline__ uint32_t chunk_state(const uint32_t (&w)[K + 1])
-{
-    constexpr int e = 32 + (Q + 1) * K;   // exclusive end bit
-    constexpr int wi = (e - 1) >> 5;      // word holding the last bit
-    constexpr int r = e & 31;             // bits of w[wi] that are used
-    if constexpr (r == 0) {
-        return w[wi] & 0xffffu;
-    } else {
-        return __builtin_amdgcn_alignbit(w[wi - 1], w[wi], 32 - r) & 0xffffu;
-    }
-}
-
-// Loads a lane's chunk: words K*c .. K*c+K-1 of the tile and the preceding word.
+// Loads a lane's chunk: w[1..K] = words K*c .. K*c+K-1 of the tile, w[0] = the word before
+// them (wrapping within the tile: the trellis is tail-biting).
 template <int K>
 __device__ __forceinline__ void load_chunk(uint32_t (&w)[K + 1], const uint32_t* __restrict__ tile, int c)
 {
@@ -91,15 +45,111 @@ __device__ __forceinline__ void load_chunk(uint32_t (&w)[K + 1], const uint32_t*
     w[0] = tile[prev];
 }
 
-// Fragment (ch, rh) of a chunk: 8 fp16 weights, element e = row 8rh + e of column c + 8ch.
+// 32-bit window of the concatenation w[0]:w[1]:...:w[K] (MSB first) ending at bit E.
+template <int K, int E>
+__device__ __forceinline__ uint32_t window(const uint32_t (&w)[K + 1])
+{
+    constexpr int wi = (E - 1) >> 5;
+    constexpr int r = E & 31;
+    if constexpr (r == 0) return w[wi];
+    else return __builtin_amdgcn_alignbit(w[wi - 1], w[wi], 32 - r);
+}
+
+// Where the 16-bit state of chunk position Q lives: the low half of the window ending at
+// bit 32 + (Q+1)K, or -- when K divides 16 -- the high half of the window ending D = 16/K
+// positions later, so that each window feeds two positions (Q and Q + D share one).
+template <int K, int Q>
+struct StateLoc {
+    static constexpr bool pairs = (16 % K) == 0;
+    static constexpr int D = pairs ? 16 / K : 1;
+    static constexpr bool hi = pairs && ((Q / D) % 2 == 0);
+    static constexpr int E = 32 + (Q + 1 + (hi ? D : 0)) * K;
+};
+
+// ---------------------------------------------------------------- codebook (VALU form)
+//
+// x = a*s + b (mod 2^32) for a 16-bit state s held in the low or high half of `src`,
+// with a = A1*2^16 + A0:  t = A0*s + b  (v_mad_u32_u16, exact 16x16+32), then
+// hi16(x) = hi16(t) + A1*s (mod 2^16)  (v_mad_u16 writing the high half of t only).
+// Both are full-rate; the masked word is then one v_bitop3_b32 ((x & m) ^ c = 0x6a).
+template <int CB, bool HI>
+__device__ __forceinline__ uint32_t cb_masked(uint32_t src)
+{
+    constexpr uint32_t A0 = CB == CB_MCG ? (0xCBAC1FEDu & 0xffffu) : (89226354u & 0xffffu);
+    constexpr uint32_t A1 = CB == CB_MCG ? (0xCBAC1FEDu >> 16) : (89226354u >> 16);
+    constexpr uint32_t B = CB == CB_MCG ? 0u : 64248484u;
+    uint32_t t;
+    if constexpr (HI) {
+        asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(t) : "v"(src), "s"(A0), "v"(B));
+        asm("v_mad_u16 %0, %1, %2, %0 op_sel:[1,0,1,1]" : "+v"(t) : "v"(src), "s"(A1));
+    } else {
+        asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(t) : "v"(src), "s"(A0), "v"(B));
+        asm("v_mad_u16 %0, %1, %2, %0 op_sel:[0,0,1,1]" : "+v"(t) : "v"(src), "s"(A1));
+    }
+    asm("v_bitop3_b32 %0, %0, %1, %2 bitop3:0x6a" : "+v"(t) : "s"(0x8FFF8FFFu), "v"(0x3B603B60u));
+    return t;
+}
+
+// Packed fp16 pair (low = weight of xa, high = weight of xb), each the IEEE fp16 sum of
+// the two halves of its masked word (SDWA adds writing one half each).
+__device__ __forceinline__ uint32_t pack_sum(uint32_t xa, uint32_t xb)
+{
+    uint32_t r;
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1"
+        : "=v"(r) : "v"(xa));
+    asm("v_add_f16_sdwa %0, %1, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1"
+        : "+v"(r) : "v"(xb));
+    return r;
+}
+
+// Masked codebook word of chunk position Q.
+template <int K, int CB, int Q>
+__device__ __forceinline__ uint32_t chunk_word(const uint32_t (&w)[K + 1])
+{
+    using L = StateLoc<K, Q>;
+    return cb_masked<CB, L::hi>(window<K, L::E>(w));
+}
+
+// Two adjacent positions Q, Q+1 as a packed fp16 pair.
+template <int K, int CB, int Q>
+__device__ __forceinline__ uint32_t chunk_pair(const uint32_t (&w)[K + 1])
+{
+    return pack_sum(chunk_word<K, CB, Q>(w), chunk_word<K, CB, Q + 1>(w));
+}
+
+// Four packed pairs (an 8-element MFMA operand) from eight masked words, in one asm block
+// that ends with two wait states: the compiler cannot see that the SDWA adds are VALU
+// writes, and an MFMA reading a VGPR needs >= 2 wait states after a VALU wrote it.
+__device__ __forceinline__ f16x8 pack_fragment(uint32_t x0, uint32_t x1, uint32_t x2, uint32_t x3,
+                                               uint32_t x4, uint32_t x5, uint32_t x6, uint32_t x7)
+{
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    uint32_t r0, r1, r2, r3;
+#define EXL3_SDWA_LO(D, S) "v_add_f16_sdwa " D ", " S ", " S " dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+#define EXL3_SDWA_HI(D, S) "v_add_f16_sdwa " D ", " S ", " S " dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 src1_sel:WORD_1\n\t"
+    asm(EXL3_SDWA_LO("%0", "%4") EXL3_SDWA_HI("%0", "%5")
+        EXL3_SDWA_LO("%1", "%6") EXL3_SDWA_HI("%1", "%7")
+        EXL3_SDWA_LO("%2", "%8") EXL3_SDWA_HI("%2", "%9")
+        EXL3_SDWA_LO("%3", "%10") EXL3_SDWA_HI("%3", "%11")
+        "s_nop 1"
+        : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+        : "v"(x0), "v"(x1), "v"(x2), "v"(x3), "v"(x4), "v"(x5), "v"(x6), "v"(x7));
+#undef EXL3_SDWA_LO
+#undef EXL3_SDWA_HI
+    u32x4 r = {r0, r1, r2, r3};
+    return __builtin_bit_cast(f16x8, r);
+}
+
+// Fragment (ch, rh) of a chunk: 8 fp16 weights, element e = row 8rh + e of column c + 8ch,
+// i.e. position q = 8(e/2) + 4ch + 2rh + e%2.
 template <int K, int CB, int CH, int RH>
 __device__ __forceinline__ f16x8 chunk_fragment(const uint32_t (&w)[K + 1])
 {
-    f16x8 f;
-#define EXL3_FE(E) f[E] = cb_value<CB>(chunk_state<K, 8 * ((E) / 2) + 4 * CH + 2 * RH + ((E) % 2)>(w));
-    EXL3_FE(0) EXL3_FE(1) EXL3_FE(2) EXL3_FE(3) EXL3_FE(4) EXL3_FE(5) EXL3_FE(6) EXL3_FE(7)
-#undef EXL3_FE
-    return f;
+    constexpr int q = 4 * CH + 2 * RH;
+    return pack_fragment(chunk_word<K, CB, q>(w), chunk_word<K, CB, q + 1>(w),
+                         chunk_word<K, CB, q + 8>(w), chunk_word<K, CB, q + 9>(w),
+                         chunk_word<K, CB, q + 16>(w), chunk_word<K, CB, q + 17>(w),
+                         chunk_word<K, CB, q + 24>(w), chunk_word<K, CB, q + 25>(w));
 }
 
 // ---------------------------------------------------------------- wave helpers

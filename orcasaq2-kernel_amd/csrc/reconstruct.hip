@@ -32,19 +32,19 @@ __global__ __launch_bounds__(64 * RC_WAVES) void reconstruct_kernel(
         const uint32_t* tile = trellis + ((long)ti * tc + tn) * (8 * K);
         uint32_t w[K + 1];
         load_chunk<K>(w, tile, c);
-        // position q = 8m + i -> row 2m + {0,1,8,9}[i%4], column c + 8(i/4)
-#define EXL3_RC(Q)                                                                         \
+        // positions q0 = 2p and q0 + 1 (p = 0..15): q0 = 8m + i, i in {0, 2, 4, 6} ->
+        // rows 2m + {0, 8}[i%4 / 2] and the row below it, column c + 8(i/4)
+#define EXL3_RC(P)                                                                         \
     {                                                                                      \
-        constexpr int m = (Q) / 8, i = (Q) % 8;                                            \
-        constexpr int row = 2 * m + ((i & 3) == 0 ? 0 : (i & 3) == 1 ? 1 : (i & 3) == 2 ? 8 : 9); \
+        constexpr int q0 = 2 * (P), m = q0 / 8, i = q0 % 8;                                \
+        constexpr int row = 2 * m + ((i & 3) == 0 ? 0 : 8);                                \
         constexpr int col8 = 8 * (i >> 2);                                                 \
-        _Float16 v = cb_value<CB>(chunk_state<K, (Q)>(w));                                 \
-        st[row * RC_STRIDE + 16 * T + c + col8] = __builtin_bit_cast(uint16_t, v);        \
+        const uint32_t v = chunk_pair<K, CB, q0>(w);                                       \
+        st[row * RC_STRIDE + 16 * T + c + col8] = (uint16_t)(v & 0xffffu);                \
+        st[(row + 1) * RC_STRIDE + 16 * T + c + col8] = (uint16_t)(v >> 16);              \
     }
         EXL3_RC(0) EXL3_RC(1) EXL3_RC(2) EXL3_RC(3) EXL3_RC(4) EXL3_RC(5) EXL3_RC(6) EXL3_RC(7)
         EXL3_RC(8) EXL3_RC(9) EXL3_RC(10) EXL3_RC(11) EXL3_RC(12) EXL3_RC(13) EXL3_RC(14) EXL3_RC(15)
-        EXL3_RC(16) EXL3_RC(17) EXL3_RC(18) EXL3_RC(19) EXL3_RC(20) EXL3_RC(21) EXL3_RC(22) EXL3_RC(23)
-        EXL3_RC(24) EXL3_RC(25) EXL3_RC(26) EXL3_RC(27) EXL3_RC(28) EXL3_RC(29) EXL3_RC(30) EXL3_RC(31)
 #undef EXL3_RC
     }
     __syncthreads();

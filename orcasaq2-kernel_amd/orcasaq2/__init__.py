@@ -17,6 +17,7 @@ Tensor parallelism is not implemented; TP > 1 raises rather than serving wrong n
 import torch
 
 from . import _native
+from . import ops  # noqa: F401  (registers orcasaq2::shard_gemm and orcasaq2::shards_gemv)
 
 BLOCK = 128
 _HAD = {}

@@ -145,19 +145,10 @@ def _vec16(fn: str, name: str, t: torch.Tensor, n: int) -> None:
 
 # ---------------------------------------------------------------- workspaces
 
-_ws: dict[tuple, torch.Tensor] = {}
-
-
-def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-initialised GEMV workspace, one per (device, stream).  The kernels leave its
-    ticket counters at zero, so it is reused by every later call on that stream."""
-    stream = torch.cuda.current_stream(device)
-    key = (device.index, stream.cuda_stream)
-    ws = _ws.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _ws[key] = ws
-    return ws
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-call scratch from torch's caching allocator (no required contents); it stays
+    alive on the stream it was allocated on until the kernels using it have run."""
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
 # ---------------------------------------------------------------- entry points
@@ -227,7 +218,7 @@ def gemv_grouped(x: torch.Tensor, shards: list[dict], out: torch.Tensor | None =
         col += oc
     L = lib()
     nbytes = L.exl3_gemv_grouped_workspace_bytes(arr, len(shards), rows, ic)
-    ws = gemv_workspace(dev, nbytes)
+    ws = workspace(dev, nbytes)
     _check(L.exl3_gemv_grouped(_ptr(x), arr, len(shards), _ptr(ws), ws.numel(), rows, ic, _stream(dev)), fn)
     return out
 
@@ -259,7 +250,7 @@ def gemm(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.T
         return out
     L = lib()
     nbytes = L.exl3_gemm_workspace_bytes(rows, ic, oc)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    ws = workspace(dev, nbytes)
     _check(L.exl3_gemm(_ptr(x), _ptr(trellis), _ptr(out), _ptr(suh), _ptr(svh), _ptr(ws), nbytes, rows, ic,
                        oc, K, codebook, _stream(dev)), fn)
     return out
