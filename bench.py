@@ -10,9 +10,13 @@ different copy of the weights (more than 512 MB of distinct packed words per K),
 resident in HBM before the timed region starts.
 
 `value` = total packed trellis bytes / total time over the timed steps.
-`roofline` = the dominant kernel (the K whose launches take the most time): algorithmic
-bytes per launch (ic*oc*K/8) / its mean launch duration from HIP events recorded on the
-launch stream inside the timed region, against 8 TB/s.
+`roofline` = the dominant GEMV (the K whose calls take the most time; one call = the
+gemv_partial_kernel<K> launch plus the small gemv_reduce_kernel launch): algorithmic bytes
+per call (ic*oc*K/8) / its mean duration from HIP events recorded on the launch stream
+inside the timed region, against 8 TB/s.  `traffic` = HBM bytes per call measured with
+rocprofv3 FETCH_SIZE + WRITE_SIZE and scaled by the same counters' reading for a plain
+copy of known size (profiles/gemv_traffic.json; `python bench.py --copy-calib` is the
+calibration workload).
 `cpu_baseline` = the reference's CPU path restated by the oracle (trellis decode in C, the
 reconstruct_weight Hadamard/sign algebra in fp32 torch, F.linear), timed on this host's
 cores on one step of the same workload.
@@ -50,6 +54,31 @@ def stack_token_bytes() -> int:
     return total
 
 
+def copy_calib(args) -> None:
+    """Plain device copy of 256 MiB, repeated: the known-size workload that calibrates the
+    FETCH_SIZE / WRITE_SIZE counters (each copy reads and writes exactly 268435456 bytes)."""
+    import torch
+    dev = torch.device("cuda", 0)
+    a = torch.empty(1 << 28, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(max(args.steps, 1)):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calib_bytes": 1 << 28, "copies": max(args.steps, 1)}), flush=True)
+
+
+def load_traffic(dom_K: int, nbytes: int):
+    """HBM bytes per GEMV call from the committed counter calibration, or None."""
+    path = os.path.join(ROOT, "profiles", "gemv_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        e = t["per_K"][str(dom_K)]
+        return int(e["hbm_bytes_per_call"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def gpu_bench(args) -> dict:
     import torch
     from orcasaq2 import _native
@@ -57,7 +86,7 @@ def gpu_bench(args) -> dict:
 
     dev = torch.device("cuda", 0)
     ic, oc = syn.INTERMEDIATE, syn.HIDDEN
-    Ks = (2, 3, 4, 5)
+    Ks = (args.only_K,) if args.only_K else (2, 3, 4, 5)
     g = torch.Generator(device=dev).manual_seed(1)
     copies = {}
     for K in Ks:
@@ -123,7 +152,8 @@ def cpu_baseline(max_seconds: float = 30.0) -> dict:
     from orcasaq2 import _t128
     from orcasaq2 import synthetic as syn
 
-    threads = os.cpu_count() or 1
+    # this host's share of cores for one GPU (the GPU boxes grant 16 per GPU)
+    threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
     ic, oc = syn.INTERMEDIATE, syn.HIDDEN
     x = syn.activations(1, ic, torch.Generator().manual_seed(11))
@@ -171,14 +201,20 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only-K", type=int, default=0, help="time a single K (profiling runs)")
+    ap.add_argument("--copy-calib", action="store_true", help="run the counter-calibration copy and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the EXL3 linear path has no "
               "multi-GPU code); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
+    if args.copy_calib:
+        copy_calib(args)
+        return
     r = gpu_bench(args)
     dom = r["per_k"][r["dom"]]
+    traffic = load_traffic(r["dom"], dom["bytes"])
     out = {
         "metric": METRIC,
         "value": round(r["value"], 2),
@@ -196,8 +232,8 @@ def main():
                                "(3INST codebook), weights rotated over >512 MB per K",
                    "hbm_frac": round(r["value"] / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dom["frac"], 4), "traffic": None,
-                     "kernel": f"exl3::gemv_kernel<{r['dom']}, 0>",
+                     "frac": round(dom["frac"], 4), "traffic": traffic,
+                     "kernel": f"exl3_gemv K={r['dom']}: gemv_partial_kernel<{r['dom']}, 0> + gemv_reduce_kernel",
                      "bytes_per_launch": dom["bytes"], "mean_launch_us": round(dom["mean_us"], 3)},
         "per_K": {str(K): {"GB/s": round(v["gbs"], 1), "frac": round(v["frac"], 4),
                            "mean_us": round(v["mean_us"], 3)} for K, v in r["per_k"].items()},

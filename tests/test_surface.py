@@ -1,0 +1,202 @@
+"""The drop-in plugin surface on the CPU (the reference's orcasaq2/config.py, heads.py and
+__init__.py behaviour), with the package's vLLM stand-ins.
+
+The product registers orcasaq2::shard_gemm / shards_gemv for the GPU only.  To drive
+Exl3LinearMethod.apply here, this module registers a CPU kernel for those ops *inside the
+test process*, computed by the CPU oracle -- the oracle is the checker, the product never
+routes through it.
+"""
+import numpy as np
+import pytest
+import torch
+
+import orcasaq2
+from orcasaq2 import _vllm_compat as vc
+from orcasaq2 import synthetic as syn
+from orcasaq2.config import SHARD_IDS, Exl3Config, Exl3LinearMethod, Exl3ShardParam, _expand
+from orcasaq2.heads import Exl3EmbeddingMethod
+from orcasaq2.ops import exl3_K
+
+
+@pytest.fixture(scope="module")
+def cpu_ops(oracle):
+    def one(x, trellis, suh, svh, oc, k, mcg, mul1):
+        y = oracle.shard_gemm_ref(x.numpy(), trellis.numpy(), suh.numpy(), svh.numpy(), int(k), 1 if mcg else 0)
+        return torch.from_numpy(y).to(torch.half)
+
+    def many(x, trellis, suh, svh, oc, k, mcg, mul1):
+        return torch.cat([one(x, *a) for a in zip(trellis, suh, svh, oc, k, mcg, mul1)], dim=1)
+
+    torch.library.register_kernel("orcasaq2::shard_gemm", "cpu", one)
+    torch.library.register_kernel("orcasaq2::shards_gemv", "cpu", many)
+    return one
+
+
+def test_exl3_K_matches_reference_semantics():
+    for last, want in [(32, 2), (48, 3), (56, 3.5), (64, 4), (80, 5), (96, 6), (24, 1.5), (40, 2.5)]:
+        k = exl3_K(torch.empty(2, 2, last))
+        assert k == want and isinstance(k, int) == float(want).is_integer()
+
+
+def test_shard_slots():
+    p = Exl3ShardParam(suffix="trellis")
+    assert p.numel() == 0 and p.suffix == "trellis"
+    assert [p.slot(s) for s in ("q", "k", "v")] == [0, 1, 2]
+    assert p.slot(None) == 0 and p.slot(1) == 1 and p.slot((2, 3)) == 2
+    with pytest.raises(ValueError, match="unknown shard id"):
+        p.slot("z")
+    assert SHARD_IDS["gate_up_proj"] == [0, 1]
+
+
+def test_config_parsing_and_manifest():
+    cfg = Exl3Config.from_config({"bits": 3.5, "tensor_storage": {
+        "model.layers.0.mlp.gate_proj": {"stored_tensors": {"model.layers.0.mlp.gate_proj.trellis": {}}},
+        "model.layers.0.linear_attn.in_proj_a": {"stored_tensors": {"x.weight": {}}}}})
+    assert cfg.get_name() == "exl3" and cfg.bits == 3.5 and cfg.codebook == "mul1" and cfg.head_bits == 16
+    assert cfg.quantized_prefixes == {"model.layers.0.mlp.gate_proj"}
+    assert Exl3Config.get_config_filenames() == ["quantization_config.json"]
+    assert torch.half in cfg.get_supported_act_dtypes() and cfg.get_min_capability() == 80
+    assert _expand("m.l.0.mlp.gate_up_proj", "gate_up_proj") == ["m.l.0.mlp.gate_proj", "m.l.0.mlp.up_proj"]
+    lin = vc.LinearBase(16, 16, quant_config=None)
+    assert isinstance(cfg.get_quant_method(lin, "model.layers.0.mlp.gate_up_proj"), Exl3LinearMethod)
+    assert isinstance(cfg.get_quant_method(lin, "model.layers.0.linear_attn.in_proj_a"), vc.UnquantizedLinearMethod)
+    assert cfg.get_quant_method(torch.nn.Linear(2, 2), "x") is None
+
+
+def test_tensor_parallel_refused():
+    cfg = Exl3Config.from_config({})
+    m = Exl3LinearMethod(cfg, "x")
+    with pytest.raises(NotImplementedError, match="tensor parallelism"):
+        m.create_weights(torch.nn.Module(), 64, [128], 128, 128, torch.half)
+
+
+def _load(layer, lins, ids):
+    for sid in ids:
+        for name in ("trellis", "suh", "svh"):
+            p = getattr(layer, name)
+            p.weight_loader(p, lins[sid][name], sid)
+
+
+def test_fused_layer_apply_matches_oracle(cpu_ops, oracle):
+    cfg = Exl3Config.from_config({"bits": 4})
+    spec = [("q", 256, 4), ("k", 128, 5), ("v", 128, 5)]
+    lins = {sid: syn.linear(128, oc, K, seed=i) for i, (sid, oc, K) in enumerate(spec)}
+    layer = vc.LinearBase(128, 512, bias=True, params_dtype=torch.float32, quant_config=cfg,
+                          prefix="model.layers.0.self_attn.qkv_proj", output_partition_sizes=[256, 128, 128])
+    _load(layer, lins, ["k", "v", "q"])
+    layer.quant_method.process_weights_after_loading(layer)
+    assert not hasattr(layer, "trellis") and layer.exl3_dense is None
+    assert [s["oc"] for s in layer.exl3_shards] == [256, 128, 128]
+    assert [s["K"] for s in layer.exl3_shards] == [4, 5, 5]
+    assert all(s["suh"].dtype == torch.half for s in layer.exl3_shards)
+    layer.bias.data = torch.randn(512)
+    for rows in (1, 3, 20):
+        x = torch.randn(rows, 128)
+        y = layer(x)
+        assert y.dtype == torch.float32 and y.shape == (rows, 512)
+        col = 0
+        for sid, oc, K in spec:
+            ref = oracle.shard_gemm_ref(x.half().numpy(), lins[sid]["trellis"], lins[sid]["suh"].numpy(),
+                                        lins[sid]["svh"].numpy(), K) + layer.bias.numpy()[col:col + oc]
+            got = y[:, col:col + oc].numpy()
+            assert np.abs(got - ref).max() <= 2e-3 * np.abs(ref).max()
+            col += oc
+
+
+def test_load_errors():
+    cfg = Exl3Config.from_config({})
+    layer = vc.LinearBase(128, 256, quant_config=cfg, prefix="p", output_partition_sizes=[128, 128])
+    lin = syn.linear(128, 128, 3, seed=0)
+    _load(layer, {0: lin}, [0])
+    with pytest.raises(RuntimeError, match="shards give 128 outputs, layer wants 256"):
+        layer.quant_method.process_weights_after_loading(layer)
+
+    layer = vc.LinearBase(128, 128, quant_config=cfg, prefix="p")
+    layer.trellis.weight_loader(layer.trellis, lin["trellis"], 0)
+    layer.weight.weight_loader(layer.weight, torch.zeros(128, 128), 1)
+    with pytest.raises(RuntimeError, match="trellis and 1 dense shards"):
+        layer.quant_method.process_weights_after_loading(layer)
+
+    layer = vc.LinearBase(128, 128, quant_config=cfg, prefix="p")
+    with pytest.raises(RuntimeError, match="no trellis and no dense weight"):
+        layer.quant_method.process_weights_after_loading(layer)
+
+
+def test_dense_fallback_layer():
+    cfg = Exl3Config.from_config({})
+    layer = vc.LinearBase(16, 24, quant_config=cfg, prefix="p", output_partition_sizes=[16, 8])
+    w0, w1 = torch.randn(16, 16), torch.randn(8, 16)
+    layer.weight.weight_loader(layer.weight, w1, 1)
+    layer.weight.weight_loader(layer.weight, w0, 0)
+    layer.quant_method.process_weights_after_loading(layer)
+    assert layer.exl3_shards is None
+    x = torch.randn(3, 16)
+    assert torch.allclose(layer(x), x @ torch.cat([w0, w1]).T)
+
+
+def test_embedding_method_load_paths():
+    cfg = Exl3Config.from_config({})
+    emb = vc.VocabParallelEmbedding(100, 8, params_dtype=torch.bfloat16, quant_config=cfg)
+    assert isinstance(emb.quant_method, Exl3EmbeddingMethod)
+    w = torch.randn(100, 8)
+    emb.weight.weight_loader(emb.weight, w)
+    emb.quant_method.process_weights_after_loading(emb)
+    ids = torch.tensor([3, 7])
+    assert torch.equal(emb(ids), w[ids])
+    # int8 table without scales
+    emb = vc.VocabParallelEmbedding(100, 8, params_dtype=torch.bfloat16, quant_config=cfg)
+    emb.qweight.weight_loader(emb.qweight, torch.zeros(100, 8, dtype=torch.int8))
+    with pytest.raises(RuntimeError, match="qweight without scales"):
+        emb.quant_method.process_weights_after_loading(emb)
+    emb = vc.VocabParallelEmbedding(100, 8, params_dtype=torch.bfloat16, quant_config=cfg)
+    with pytest.raises(RuntimeError, match="neither an int8 table nor a dense one"):
+        emb.quant_method.process_weights_after_loading(emb)
+    # tied-head apply dequantizes the int8 table
+    emb = vc.VocabParallelEmbedding(100, 8, params_dtype=torch.float32, quant_config=cfg)
+    q = torch.randint(-128, 128, (100, 8), dtype=torch.int8)
+    s = torch.rand(100)
+    emb.qweight.weight_loader(emb.qweight, q)
+    emb.scales.weight_loader(emb.scales, s)
+    emb.quant_method.process_weights_after_loading(emb)
+    x = torch.randn(2, 8)
+    want = x @ (q.float() * s[:, None]).T
+    assert torch.allclose(emb.quant_method.apply(emb, x), want, atol=1e-5)
+
+
+def test_lm_head_gets_linear_method():
+    cfg = Exl3Config.from_config({"head_bits": 6})
+    assert isinstance(cfg.get_quant_method(object.__new__(vc.ParallelLMHead), "lm_head"), Exl3LinearMethod)
+
+
+def test_register_and_patch_embedding_constructors(native):
+    orcasaq2.register()
+    assert vc.quant_registry()["exl3"] is Exl3Config
+    orcasaq2.register()  # idempotent
+    assert getattr(vc.VocabParallelEmbedding, "_orca_patched", False)
+    cfg = Exl3Config.from_config({})
+
+    class Cfg:
+        quant_config = cfg
+
+    with vc.set_current_vllm_config(Cfg()):
+        emb = vc.VocabParallelEmbedding(64, 8)            # model code passes no quant_config
+        head = vc.ParallelLMHead(64, 8, prefix="lm_head")  # forwards it positionally
+    assert isinstance(emb.quant_method, Exl3EmbeddingMethod)
+    assert isinstance(head.quant_method, Exl3LinearMethod)
+    plain = vc.VocabParallelEmbedding(64, 8)              # no current EXL3 config: untouched
+    assert plain.quant_method is None
+
+
+def test_product_op_has_no_cpu_path_without_the_test_kernel():
+    import subprocess
+    import sys
+    code = ("import sys; sys.path.insert(0, 'orcasaq2-kernel_amd'); import torch, orcasaq2\n"
+            "x = torch.zeros(1, 128, dtype=torch.half); t = torch.zeros(8, 8, 64, dtype=torch.int16)\n"
+            "s = torch.ones(128, dtype=torch.half)\n"
+            "try:\n torch.ops.orcasaq2.shard_gemm(x, t, s, s, 128, 4.0, False, False)\nexcept Exception as e:\n"
+            " print(type(e).__name__); sys.exit(0)\nsys.exit(1)\n")
+    import os
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "NotImplementedError" in r.stdout or "RuntimeError" in r.stdout
