@@ -56,7 +56,7 @@ extern "C" {
 
 const char* exl3_last_error(void) { return g_err; }
 
-int exl3_abi_version(void) { return 1; }
+int exl3_abi_version(void) { return 2; }
 
 int exl3_reconstruct(void* W, const void* trellis, int ic, int oc, int K, int codebook, void* stream)
 {
@@ -90,13 +90,17 @@ int exl3_had_r_128(const void* in, void* out, const void* pre, const void* post,
 size_t exl3_gemv_workspace_bytes(int rows, int ic, int oc)
 {
     if (rows < 1 || ic < 128 || oc < 128) return 0;
-    return gemv_workspace_bytes(rows, ic, oc);
+    return GEMV_COUNTER_BYTES + gemv_workspace_bytes(rows, ic, oc);
 }
 
 size_t exl3_gemv_grouped_workspace_bytes(const exl3_shard_t* shards, int nshards, int rows, int ic)
 {
-    size_t t = 0;
-    for (int i = 0; shards && i < nshards; i++) t += exl3_gemv_workspace_bytes(rows, ic, shards[i].oc);
+    if (!shards || nshards < 1 || rows < 1 || ic < 128) return 0;
+    size_t t = GEMV_COUNTER_BYTES;
+    for (int i = 0; i < nshards; i++) {
+        if (shards[i].oc < 128) return 0;
+        t += gemv_workspace_bytes(rows, ic, shards[i].oc);
+    }
     return t;
 }
 

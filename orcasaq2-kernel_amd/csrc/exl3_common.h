@@ -25,6 +25,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace exl3 {
 
 enum Codebook : int { CB_3INST = 0, CB_MCG = 1, CB_MUL1 = 2 };
@@ -207,6 +209,188 @@ __device__ __forceinline__ f16x8 chunk_hfragment(const uint32_t (&w)[K + 1], con
     u32x4 r = {chunk_hword<K, CB, q>(w, k), chunk_hword<K, CB, q + 1>(w, k),
                chunk_hword<K, CB, q + 2>(w, k), chunk_hword<K, CB, q + 3>(w, k)};
     return __builtin_bit_cast(f16x8, r);
+}
+
+// ---------------------------------------------------------------- codebook (batch-1 dot2 form)
+//
+// 3INST in offset form: a = 89226354 and b = 64248484 are both even, so with
+// C = (b/2) * (a/2)^-1 mod 2^31 = 0x68b437e2,  a*s + b = a*(s + C) (mod 2^32) for every
+// 16-bit state s.  One SDWA add then both takes the state out of the low or high half of
+// a 32-bit register and adds C, and one v_mul_lo_u32 finishes x -- two VALU ops where the
+// clean-shift / multiply / add form needs three.  MCG (b = 0) multiplies the clean state.
+constexpr uint32_t CB3_OFFSET = 0x68b437e2u;
+
+// Where chunk position Q's 16-bit state is taken from.  E = stream end bit (exclusive) of
+// the state inside w[0]:w[1]:..:w[K] (MSB first), word wi = (E-1)/32, r = E%32:
+//   0: low half of w[wi] (r = 0)            1: high half of w[wi] (r = 16)
+//   2: low half of the window ending at E    (straddles a word boundary; K | 16)
+//   3: high half of the window ending at E+16 (inside w[wi]; K | 16; that window is the
+//      kind-2 window of position Q + 16/K, so the two share one v_alignbit)
+//   4: low half of w[wi] >> (32 - r)          (inside w[wi])
+//   5: low half of W16 >> (16 - r), W16 = the 32 bits centred on the boundary before
+//      w[wi] (straddles; K not dividing 16: one v_alignbit per boundary)
+template <int K, int Q>
+struct StatePlan {
+    static constexpr int E = 32 + (Q + 1) * K;
+    static constexpr int wi = (E - 1) >> 5;
+    static constexpr int r = E & 31;
+    static constexpr bool pairs = (16 % K) == 0;
+    static constexpr int kind = r == 0 ? 0 : r == 16 ? 1
+        : (r < 16 ? (pairs ? 2 : 5) : ((pairs && E + 16 <= 32 * (K + 1)) ? 3 : 4));
+};
+
+template <int K, int Q>
+__device__ __forceinline__ uint32_t state_src(const uint32_t (&w)[K + 1])
+{
+    using P = StatePlan<K, Q>;
+    if constexpr (P::kind == 0 || P::kind == 1) return w[P::wi];
+    else if constexpr (P::kind == 2) return window<K, P::E>(w);
+    else if constexpr (P::kind == 3) return window<K, P::E + 16>(w);
+    else if constexpr (P::kind == 4) return w[P::wi] >> (32 - P::r);
+    else return window<K, 32 * P::wi + 16>(w) >> (16 - P::r);
+}
+
+__device__ __forceinline__ uint32_t sdwa_add_lo(uint32_t v, uint32_t c)
+{
+    uint32_t d;
+    asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 src1_sel:DWORD"
+        : "=v"(d) : "v"(v), "v"(c));
+    return d;
+}
+
+__device__ __forceinline__ uint32_t sdwa_add_hi(uint32_t v, uint32_t c)
+{
+    uint32_t d;
+    asm("v_add_u32_sdwa %0, %1, %2 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1 src1_sel:DWORD"
+        : "=v"(d) : "v"(v), "v"(c));
+    return d;
+}
+
+struct Dot2Consts {
+    uint32_t mask, flip, off;   // 0x8FFF8FFF, 0x3B603B60, CB3_OFFSET pinned in VGPRs
+};
+
+__device__ __forceinline__ Dot2Consts dot2_consts()
+{
+    Dot2Consts k;
+    asm volatile("v_mov_b32 %0, 0x8fff8fff" : "=v"(k.mask));
+    asm volatile("v_mov_b32 %0, 0x3b603b60" : "=v"(k.flip));
+    asm volatile("v_mov_b32 %0, 0x68b437e2" : "=v"(k.off));
+    return k;
+}
+
+// Masked codebook word of chunk position Q.
+template <int K, int CB, int Q>
+__device__ __forceinline__ uint32_t dot2_word(const uint32_t (&w)[K + 1], const Dot2Consts& k)
+{
+    using P = StatePlan<K, Q>;
+    const uint32_t src = state_src<K, Q>(w);
+    uint32_t x;
+    if constexpr (CB == CB_MCG) {
+        const uint32_t s = (P::kind == 1 || P::kind == 3) ? (src >> 16) : (src & 0xffffu);
+        x = s * 0xCBAC1FEDu;
+    } else {
+        const uint32_t s = (P::kind == 1 || P::kind == 3) ? sdwa_add_hi(src, k.off) : sdwa_add_lo(src, k.off);
+        x = s * 89226354u;
+    }
+    return (x & k.mask) ^ k.flip;
+}
+
+__device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c)
+{
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+}
+
+// One tile row's 16 activations, fp16(H128(x * suh)) rows 16a .. 16a+15 of its 128-input
+// block, from the block's inputs spread as lane l = x[2l], x[2l+1] (and suh alike).  In
+// Sylvester order H128 = H8 (x) H16: row 16a + b, input 16c + d has sign
+// H8[a][c] H16[b][d], so the 16 outputs are H16 of the eight inputs rows summed with the
+// signs H8[a][c] (c = lane / 8) -- a cross-lane sum over lanes 8 apart, then a 16-point
+// butterfly over d = 2(lane % 8) + k.  The result: lane l (in every 16-lane row) holds
+// fp16 (v, v) of rows 2(l % 8) (d0) and 2(l % 8) + 1 (d1).
+// sign_factor(a, lane) = H8[a][lane / 8] / sqrt(128): the per-lane factor for tile row a.
+__device__ __forceinline__ float tile_row_factor(int a, int lane)
+{
+    return (__builtin_popcount(a & (lane >> 3)) & 1) ? -0.08838834764831845f : 0.08838834764831845f;
+}
+
+__device__ __forceinline__ void tile_row_act(uint32_t xw, uint32_t sw, float f, int lane, uint32_t& d0, uint32_t& d1)
+{
+    typedef _Float16 h2v __attribute__((ext_vector_type(2)));
+    const h2v xh = __builtin_bit_cast(h2v, xw), sh = __builtin_bit_cast(h2v, sw);
+    float u0 = (float)xh.x * (float)sh.x * f, u1 = (float)xh.y * (float)sh.y * f;
+    u0 += __shfl_xor(u0, 8, 64);
+    u1 += __shfl_xor(u1, 8, 64);
+    u0 += __shfl_xor(u0, 16, 64);
+    u1 += __shfl_xor(u1, 16, 64);
+    u0 += __shfl_xor(u0, 32, 64);
+    u1 += __shfl_xor(u1, 32, 64);
+    float t0 = u0 + u1, t1 = u0 - u1;
+#pragma unroll
+    for (int bit = 1; bit < 8; bit <<= 1) {
+        const float p0 = __shfl_xor(t0, bit, 64), p1 = __shfl_xor(t1, bit, 64);
+        const float sg = (lane & bit) ? -1.f : 1.f;
+        t0 = p0 + sg * t0;
+        t1 = p1 + sg * t1;
+    }
+    const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)t0), h1 = __builtin_bit_cast(uint16_t, (_Float16)t1);
+    d0 = h0 | (h0 << 16);
+    d1 = h1 | (h1 << 16);
+}
+
+// One lane's chunk (32 positions) against one tile row of activations (tile_row_act's
+// layout): position q = 8m + i sits in tile row r = 2m + {0, 1, 8, 9}[i % 4], whose
+// activation DPP broadcasts (row_newbcast) from lane r / 2 of d_{r % 2} straight into
+// v_dot2c: both fp16 halves of the masked word are multiplied by the activation and
+// summed in fp32, so the weight's fp16 half-sum is never rounded.  acc[2*(i/4) + (m&1)]
+// collects column c + 8*(i/4) of the lane's tile.
+template <int Q>
+struct Dot2Pos {
+    static constexpr int m = Q / 8, i = Q % 8;
+    static constexpr int slot = 2 * (i / 4) + (m & 1);
+    static constexpr int r = 2 * m + ((i & 3) == 0 ? 0 : (i & 3) == 1 ? 1 : (i & 3) == 2 ? 8 : 9);
+};
+
+// Positions 4G .. 4G+3 share m and column half (slot); their rows 2m + {0,1,8,9} read lanes
+// m, m, m+4, m+4 of d0, d1, d0, d1.  DPP reads of a VGPR need two wait states after a VALU
+// write of it and the compiler does not track hazards inside inline asm, so each block of
+// four starts with s_nop 1.
+template <int K, int CB, int G>
+__device__ __forceinline__ void dot2_quad(const uint32_t (&w)[K + 1], uint32_t d0, uint32_t d1, float (&acc)[4],
+                                          const Dot2Consts& k)
+{
+    using P = Dot2Pos<4 * G>;
+    static_assert(Dot2Pos<4 * G + 3>::slot == P::slot, "a quad shares one accumulator");
+    const uint32_t q0 = dot2_word<K, CB, 4 * G>(w, k), q1 = dot2_word<K, CB, 4 * G + 1>(w, k);
+    const uint32_t q2 = dot2_word<K, CB, 4 * G + 2>(w, k), q3 = dot2_word<K, CB, 4 * G + 3>(w, k);
+    asm("s_nop 1\n\t"
+        "v_dot2c_f32_f16_dpp %0, %1, %3 row_newbcast:%7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %0, %2, %4 row_newbcast:%7 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %0, %1, %5 row_newbcast:%8 row_mask:0xf bank_mask:0xf\n\t"
+        "v_dot2c_f32_f16_dpp %0, %2, %6 row_newbcast:%8 row_mask:0xf bank_mask:0xf"
+        : "+v"(acc[P::slot])
+        : "v"(d0), "v"(d1), "v"(q0), "v"(q1), "v"(q2), "v"(q3), "i"(P::m), "i"(P::m + 4));
+}
+
+template <int K, int CB, int... Gs>
+__device__ __forceinline__ void dot2_chunk_seq(const uint32_t (&w)[K + 1], uint32_t d0, uint32_t d1, float (&acc)[4],
+                                               const Dot2Consts& k, std::integer_sequence<int, Gs...>)
+{
+    (dot2_quad<K, CB, Gs>(w, d0, d1, acc, k), ...);
+}
+
+// One lane's chunk (32 positions) against one tile row of activations (tile_row_act's
+// layout): position q = 8m + i sits in tile row r = 2m + {0, 1, 8, 9}[i % 4], whose
+// activation DPP broadcasts (row_newbcast) from lane r / 2 of d_{r % 2} straight into
+// v_dot2c: both fp16 halves of the masked word are multiplied by the activation and
+// summed in fp32, so the weight's fp16 half-sum is never rounded.  acc[2*(i/4) + (m&1)]
+// collects column c + 8*(i/4) of the lane's tile.
+template <int K, int CB>
+__device__ __forceinline__ void dot2_chunk(const uint32_t (&w)[K + 1], uint32_t d0, uint32_t d1, float (&acc)[4],
+                                           const Dot2Consts& k)
+{
+    dot2_chunk_seq<K, CB>(w, d0, d1, acc, k, std::make_integer_sequence<int, 8>{});
 }
 
 // ---------------------------------------------------------------- wave helpers

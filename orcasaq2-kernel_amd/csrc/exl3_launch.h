@@ -29,7 +29,14 @@ struct GemvShard {
     long ldc;
 };
 
+// Start of every GEMV workspace: one u32 counter per column group of a batch-1 launch,
+// zero before the first call and left zero by every call (the batch-1 kernel resets the
+// counters it uses).  Partial-sum buffers of all GEMV paths start after it.
+constexpr size_t GEMV_COUNTER_BYTES = 16384;
 size_t gemv_workspace_bytes(int rows, int ic, int oc);
+size_t gemv1_slot_bytes(int ic, int oc);
+int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint32_t* counters, int max_counters,
+                   char* slots, size_t slot_bytes, hipStream_t stream);
 int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows,
                   void* workspace, size_t ws_bytes, hipStream_t stream);
 size_t gemm_workspace_bytes(int rows, int ic, int oc);

@@ -65,8 +65,10 @@ static inline int gemv_splits(int ic, int oc)
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Per-shard share of a GEMV workspace (the counter area is added once per call).
 size_t gemv_workspace_bytes(int rows, int ic, int oc)
 {
+    if (rows == 1) return align256(gemv1_slot_bytes(ic, oc));
     return align256((size_t)gemv_splits(ic, oc) * rows * oc * sizeof(float));
 }
 
@@ -285,13 +287,17 @@ int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int r
     if (rows < 1 || rows > GV_MAX_ROWS)
         return set_error(EXL3_ERR_ARG, "exl3_gemv: rows=%d is not in 1..%d", rows, GV_MAX_ROWS);
     size_t offs[EXL3_MAX_SHARDS + 1];
-    offs[0] = 0;
+    offs[0] = GEMV_COUNTER_BYTES;
     for (int i = 0; i < nshards; i++) offs[i + 1] = offs[i] + gemv_workspace_bytes(rows, shards[i].ic, shards[i].oc);
     if (ws_bytes < offs[nshards])
         return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: workspace of %zu bytes, %zu needed", ws_bytes,
                          offs[nshards]);
 
     char* ws = static_cast<char*>(workspace);
+    if (rows == 1)
+        return gemv1_dispatch(A, shards, nshards, reinterpret_cast<uint32_t*>(ws),
+                              (int)(GEMV_COUNTER_BYTES / sizeof(uint32_t)), ws + GEMV_COUNTER_BYTES,
+                              offs[nshards] - GEMV_COUNTER_BYTES, stream);
     bool done[EXL3_MAX_SHARDS] = {false};
     const size_t lds = hx_bytes(rows);
     for (int i = 0; i < nshards; i++) {

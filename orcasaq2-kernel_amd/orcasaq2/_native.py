@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libexl3hip.so"
 LIB_PATH = os.environ.get("ORCASAQ2_LIB", os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME))
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 CB_3INST, CB_MCG, CB_MUL1 = 0, 1, 2
 GEMV_MAX_ROWS = 16
@@ -151,6 +151,24 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
+_gemv_ws: dict = {}
+
+
+def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The GEMV workspace of (device, current stream): zero-filled when created and kept
+    zero in its counter area by every call (exl3hip.h), so it persists across calls and is
+    reused -- also by HIP-graph replays of captured calls.  Calls on one stream run in
+    order, so they can share it; another stream gets its own.  A call needing more gets a
+    larger zeroed buffer; the old one is released in stream order."""
+    stream = torch.cuda.current_stream(device).cuda_stream
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _gemv_ws.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _gemv_ws[key] = ws
+    return ws
+
+
 # ---------------------------------------------------------------- entry points
 
 def reconstruct(trellis: torch.Tensor, K, codebook: int, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -218,7 +236,7 @@ def gemv_grouped(x: torch.Tensor, shards: list[dict], out: torch.Tensor | None =
         col += oc
     L = lib()
     nbytes = L.exl3_gemv_grouped_workspace_bytes(arr, len(shards), rows, ic)
-    ws = workspace(dev, nbytes)
+    ws = gemv_workspace(dev, nbytes)
     _check(L.exl3_gemv_grouped(_ptr(x), arr, len(shards), _ptr(ws), ws.numel(), rows, ic, _stream(dev)), fn)
     return out
 

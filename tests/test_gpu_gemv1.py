@@ -1,0 +1,96 @@
+"""GPU parity of the batch-1 decode-GEMV (one activation row), through the C ABI.
+
+The batch-1 kernel cuts a launch's tile-row units into equal contiguous ranges, one per
+workgroup, so one column group can be split over several workgroups and one workgroup can
+touch several column groups (and shards).  These cases cover: a column group inside one
+workgroup, split over several, workgroups spanning 2-3 column groups and a shard
+boundary, waves left without units, every K and both codebooks, grouped shards with mixed
+K, the segment counters left at zero for the next call, determinism, and the config-4
+lm_head shape (5120 -> 151936, K = 6) checked on sampled column groups.  Bar: per-row
+relative L2 error <= 1e-3 against the fp64 oracle on the same fp16 inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+from orcasaq2 import synthetic as syn
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+
+
+def dev():
+    return torch.device("cuda", 0)
+
+
+def to_gpu(d):
+    return {k: (v.to(dev()) if isinstance(v, torch.Tensor) else v) for k, v in d.items()}
+
+
+def check(y, x, lin, cb, oracle):
+    ref = oracle.shard_gemm_ref(x.numpy(), lin["trellis"], lin["suh"].numpy(), lin["svh"].numpy(), lin["K"], cb)
+    err = oracle.rel_err_rows(y.detach().cpu().numpy(), ref)
+    assert err.max() <= REL_TOL, err.max()
+
+
+@pytest.mark.parametrize("ic,oc", [(128, 128), (256, 1024), (1024, 128), (640, 3200), (5120, 1024),
+                                   (2048, 2048)])
+@pytest.mark.parametrize("K", [2, 3, 4, 5])
+def test_gemv1_shapes(native, oracle, ic, oc, K):
+    lin = syn.linear(ic, oc, K, seed=ic + oc + K)
+    x = syn.activations(1, ic, torch.Generator().manual_seed(K))
+    d = to_gpu(lin)
+    y = native.gemv(x.to(dev()), d["trellis"], d["suh"], d["svh"], K, 0)
+    check(y, x, lin, 0, oracle)
+
+
+@pytest.mark.parametrize("K", [1, 6, 7, 8])
+@pytest.mark.parametrize("cb", [0, 1])
+def test_gemv1_other_K_and_mcg(native, oracle, K, cb):
+    lin = syn.linear(768, 1536, K, seed=50 + K)
+    x = syn.activations(1, 768, torch.Generator().manual_seed(K + 10 * cb))
+    d = to_gpu(lin)
+    y = native.gemv(x.to(dev()), d["trellis"], d["suh"], d["svh"], K, cb)
+    check(y, x, lin, cb, oracle)
+
+
+def test_gemv1_grouped_mixed_K(native, oracle):
+    """Four shards, three with K=3 (one launch: workgroups cross shard boundaries) and one
+    with K=5 (its own launch), written side by side."""
+    spec = [(384, 3), (1024, 3), (128, 5), (2560, 3)]
+    lins = [syn.linear(1024, oc, K, seed=300 + i) for i, (oc, K) in enumerate(spec)]
+    x = syn.activations(1, 1024, torch.Generator().manual_seed(31))
+    y = native.gemv_grouped(x.to(dev()), [dict(to_gpu(l), codebook=0) for l in lins])
+    col = 0
+    for l in lins:
+        check(y[:, col:col + l["oc"]], x, l, 0, oracle)
+        col += l["oc"]
+
+
+def test_gemv1_counters_left_zero_and_deterministic(native):
+    lin = to_gpu(syn.linear(4096, 2048, 4, seed=77))
+    x = syn.activations(1, 4096, torch.Generator().manual_seed(7)).to(dev())
+    ys = [native.gemv(x, lin["trellis"], lin["suh"], lin["svh"], 4, 0) for _ in range(5)]
+    torch.cuda.synchronize()
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
+    key = (0, torch.cuda.current_stream(dev()).cuda_stream)
+    ws = native._gemv_ws[key]
+    assert int(ws[:16384].count_nonzero()) == 0
+
+
+def test_gemv1_lm_head_sampled_column_groups(native, oracle):
+    """Config-4 lm_head, 5120 -> 151936 at K=6 (1187 column groups, three per workgroup
+    range): compare four column groups with the oracle on the matching trellis slice."""
+    ic, oc, K = 5120, 151936, 6
+    g = torch.Generator().manual_seed(4)
+    t = syn.trellis(ic, oc, K, g)
+    suh = syn.signs(ic, g)
+    svh = syn.svh(ic, oc, g)
+    x = syn.activations(1, ic, torch.Generator().manual_seed(41))
+    y = native.gemv(x.to(dev()), t.to(dev()), suh.to(dev()), svh.to(dev()), K, 0).cpu()
+    for cg in (0, 1, 593, 1186):
+        sl = slice(cg * 128, (cg + 1) * 128)
+        lin = dict(trellis=t[:, cg * 8:(cg + 1) * 8].contiguous(), suh=suh, svh=svh[sl].contiguous(), K=K)
+        check(y[:, sl], x, lin, 0, oracle)
