@@ -9,11 +9,14 @@ different copy of the weights (more than 512 MB of distinct packed words per K),
 256 MB Infinity Cache cannot serve a repeat: the bytes come from HBM.  Inputs are
 resident in HBM before the timed region starts.
 
+The timed steps are replayed from a HIP graph (captured once, the way decode serving
+replays its steps), so host launch overhead is not part of the measurement; the
+warm-up steps are a graph replay too.
 `value` = total packed trellis bytes / total time over the timed steps.
-`roofline` = the dominant GEMV (the K whose calls take the most time; one call = the
-gemv_partial_kernel<K> launch plus the small gemv_reduce_kernel launch): algorithmic bytes
-per call (ic*oc*K/8) / its mean duration from HIP events recorded on the launch stream
-inside the timed region, against 8 TB/s.  `traffic` = HBM bytes per call measured with
+`roofline` = the dominant GEMV (the K whose calls take the most time; one call = one
+gemv1_kernel<K> launch): algorithmic bytes per call (ic*oc*K/8) / its mean duration from
+HIP events recorded on the replay stream around a graph of the same steps, against
+8 TB/s.  `traffic` = HBM bytes per call measured with
 rocprofv3 FETCH_SIZE + WRITE_SIZE and scaled by the same counters' reading for a plain
 copy of known size (profiles/gemv_traffic.json; `python bench.py --copy-calib` is the
 calibration workload).
@@ -80,6 +83,11 @@ def load_traffic(dom_K: int, nbytes: int):
 
 
 def gpu_bench(args) -> dict:
+    """Config 1 on the GPU.  Each step is captured once into a HIP graph (the way decode
+    serving replays its steps) so host launch overhead is outside the measurement: W
+    warm-up steps are one graph replay, the K timed steps another, bracketed by
+    synchronisation.  Per-K figures come from one graph per K, timed with HIP events on
+    the capture stream."""
     import torch
     from orcasaq2 import _native
     from orcasaq2 import synthetic as syn
@@ -103,38 +111,57 @@ def gpu_bench(args) -> dict:
         copies[K] = lst
     x = torch.randn(1, ic, generator=g, device=dev).half()
     outs = {K: torch.empty(1, oc, dtype=torch.half, device=dev) for K in Ks}
-    stream = torch.cuda.current_stream(dev)
 
-    def run(step: int, events=None):
-        for K in Ks:
-            t, suh, svh = copies[K][step % len(copies[K])]
-            if events is not None:
-                events[K].append(torch.cuda.Event(enable_timing=True))
-                events[K][-1].record(stream)
-            _native.gemv(x, t, suh, svh, K, 0, out=outs[K])
-            if events is not None:
-                events[K].append(torch.cuda.Event(enable_timing=True))
-                events[K][-1].record(stream)
+    def gemv(K, step):
+        t, suh, svh = copies[K][step % len(copies[K])]
+        _native.gemv(x, t, suh, svh, K, 0, out=outs[K])
 
-    for i in range(args.warmup):
-        run(i)
+    def run_steps(first, count, only=None):
+        for i in range(first, first + count):
+            for K in (only or Ks):
+                gemv(K, i)
+
+    # eager calls first: they allocate the persistent workspace outside any capture
+    run_steps(0, 2)
     torch.cuda.synchronize()
-    events = {K: [] for K in Ks}
+    side = torch.cuda.Stream(dev)
+
+    def capture(first, count, only=None):
+        graph = torch.cuda.CUDAGraph()
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            run_steps(first, 1, only)   # settles this stream's workspace before capture
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                run_steps(first, count, only)
+        torch.cuda.synchronize()
+        return graph
+
+    g_warm = capture(0, max(args.warmup, 1))
+    g_timed = capture(args.warmup, args.steps)
+    g_warm.replay()
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(args.steps):
-        run(args.warmup + i, events)
+    g_timed.replay()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
     per_k = {}
     for K in Ks:
-        ev = events[K]
-        durs = [ev[2 * i].elapsed_time(ev[2 * i + 1]) * 1e-3 for i in range(args.steps)]
+        gk = capture(args.warmup, args.steps, only=(K,))
+        gk.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(side)
+        with torch.cuda.stream(side):
+            gk.replay()
+        e1.record(side)
+        torch.cuda.synchronize()
+        mean = e0.elapsed_time(e1) * 1e-3 / args.steps
         nbytes = syn.packed_bytes(ic, oc, K)
-        mean = sum(durs) / len(durs)
-        per_k[K] = dict(bytes=nbytes, mean_us=mean * 1e6, median_us=statistics.median(durs) * 1e6,
-                        gbs=nbytes / mean / 1e9, frac=nbytes / mean / 1e9 / HBM_PEAK_GBS,
-                        total_s=sum(durs))
+        per_k[K] = dict(bytes=nbytes, mean_us=mean * 1e6, gbs=nbytes / mean / 1e9,
+                        frac=nbytes / mean / 1e9 / HBM_PEAK_GBS, total_s=mean * args.steps)
+        del gk
     total_bytes = sum(per_k[K]["bytes"] for K in Ks) * args.steps
     value = total_bytes / wall / 1e9
     dom = max(Ks, key=lambda K: per_k[K]["total_s"])
@@ -233,7 +260,7 @@ def main():
                    "hbm_frac": round(r["value"] / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["frac"], 4), "traffic": traffic,
-                     "kernel": f"exl3_gemv K={r['dom']}: gemv_partial_kernel<{r['dom']}, 0> + gemv_reduce_kernel",
+                     "kernel": f"exl3_gemv K={r['dom']}: gemv1_kernel<{r['dom']}, 0> (one launch per call)",
                      "bytes_per_launch": dom["bytes"], "mean_launch_us": round(dom["mean_us"], 3)},
         "per_K": {str(K): {"GB/s": round(v["gbs"], 1), "frac": round(v["frac"], 4),
                            "mean_us": round(v["mean_us"], 3)} for K, v in r["per_k"].items()},
