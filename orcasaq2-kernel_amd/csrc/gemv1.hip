@@ -13,14 +13,17 @@
 // *segments* (shard, column group); its waves take the range's units round-robin.
 //
 // Per workgroup:
-//   1. each wave issues the loads of its first two units (so HBM is busy from the start),
-//      then the waves build fp16(H(x * suh)) for the 128-input blocks the range needs, as
-//      duplicated (x, x) fp16 pairs in LDS (FWHT in registers + cross-lane shuffles);
-//   2. main loop: a unit's K words (+ the tail-biting word before them) per lane stream
-//      through a two-deep register ring; each position is decoded with an SDWA add, a
-//      v_mul_lo_u32 and a v_bitop3, and its masked word meets the activation in a v_dot2
-//      (both fp16 halves times x, summed in fp32).  The tile row's 16 activations are
-//      LDS broadcast reads;
+//   1. each wave issues the loads of its first D units (D = 2..6 by K, about 24 VGPRs of
+//      words in flight per lane), so HBM is busy from the start;
+//   2. main loop over the wave's units: a unit's K words (+ the tail-biting word before
+//      them) per lane stream through the D-deep register ring.  The tile row's 16
+//      activations fp16(H(x * suh)) are built in registers from the 128-input block (one
+//      x and one suh dword per lane; per-lane sign factor, cross-lane shuffles over lane
+//      bits 3..5, butterflies over lane bits 0..2), one unit ahead of its use.  Each
+//      position is decoded with an SDWA add (or a 16-bit field for MCG), a v_mul_lo_u32 and
+//      a v_bitop3; the masked word meets its activation in a v_dot2c_f32_f16 whose second
+//      operand is broadcast by DPP from the lane that owns the activation row (both fp16
+//      halves times x, summed in fp32);
 //   3. per segment, the waves' partial sums are added in a fixed order through LDS.  If the
 //      segment lies inside this workgroup's range it is finished here; otherwise the
 //      partial goes to this workgroup's slot with agent-coherent stores, and the last of the
@@ -111,9 +114,8 @@ __device__ __forceinline__ void g1_load(uint32_t (&w)[K + 1], const uint32_t* __
     w[0] = unit[lprev];
 }
 
-// Eight waves per SIMD need at most 64 VGPRs and -- measured on MI355X, whatever the
-// occupancy API reports -- at most ~74 SGPRs: above that a CU holds only 3 of these
-// workgroups and a quarter of the grid runs as a second round.
+// Eight waves per SIMD need at most 64 VGPRs (measured on MI355X: 68 VGPRs leave room for
+// only 6); the SGPR cap keeps the count well inside what eight waves per SIMD may hold.
 template <int K, int CB>
 __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8), amdgpu_num_sgpr(74))) void gemv1_kernel(const G1Args a)
 {
