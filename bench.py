@@ -1,7 +1,7 @@
 """Benchmark of the MI355X EXL3 trellis linear path (BASELINE.json metric):
 bs=1 fused EXL3 GEMV, packed-weight GB/s and fraction of HBM peak.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--workload config1]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-stack]
 
 Workload: down_proj 17408 -> 5120 at batch 1 through the fused
 decode-GEMV at K = 2, 3, 4 and 5 bits.  One step = one GEMV at each K.  Every GEMV reads a
@@ -23,6 +23,12 @@ calibration workload).
 `cpu_baseline` = the reference's CPU path restated by the oracle (trellis decode in C, the
 reconstruct_weight Hadamard/sign algebra in fp32 torch, F.linear), timed on this host's
 cores on one step of the same workload.
+`tok_s_equiv` / `stack` = config 4 measured: the whole 64-layer linear stack + lm_head +
+embedding gather of one batch-1 token as one HIP graph, replayed (attention excluded).
+
+    python bench.py --workload config2   # grouped qkv / gate_up GEMVs at batch 1, 4, 16
+    python bench.py --workload config3   # M=2048 prefill GEMM (TFLOP/s, MFMA share) + reconstruct
+print their own JSON line instead of the headline line.
 """
 from __future__ import annotations
 
@@ -40,21 +46,8 @@ sys.path.insert(0, ROOT)
 
 METRIC = "bs=1 fused EXL3 GEMV packed-weight GB/s (% HBM peak) + 27B tok/s-equiv"
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFS = 2500.0   # dense fp16 MFMA, MI355X
 ROTATE_BYTES = 600 * 2 ** 20
-STACK_BYTES_PER_TOKEN = None  # filled from the seeded config-4 draw
-
-
-def stack_token_bytes() -> int:
-    from orcasaq2 import synthetic as syn
-    shapes = syn.stack_shapes()
-    total = 0
-    for layer in syn.stack_bits():
-        for name, K in layer.items():
-            ic, oc = shapes[name]
-            total += syn.packed_bytes(ic, oc, K)
-    total += syn.packed_bytes(syn.HIDDEN, syn.VOCAB, 6)  # K=6 lm_head
-    total += syn.HIDDEN + 2                            # int8 embedding row + its scale
-    return total
 
 
 def copy_calib(args) -> None:
@@ -165,9 +158,179 @@ def gpu_bench(args) -> dict:
     total_bytes = sum(per_k[K]["bytes"] for K in Ks) * args.steps
     value = total_bytes / wall / 1e9
     dom = max(Ks, key=lambda K: per_k[K]["total_s"])
-    tok_bytes = stack_token_bytes()
-    return dict(value=value, wall=wall, per_k=per_k, dom=dom, tok_bytes=tok_bytes,
+    return dict(value=value, wall=wall, per_k=per_k, dom=dom,
                 device=torch.cuda.get_device_name(dev))
+
+
+def _rand_linear(ic, oc, K, g, dev):
+    """One synthetic EXL3 tensor set made on the GPU (same distributions as
+    orcasaq2.synthetic: uniform 16-bit trellis words, +-1 suh, +-|N(0,1)|/sqrt(ic) svh)."""
+    import torch
+    t = torch.randint(-32768, 32768, (ic // 16, oc // 16, 16 * K), generator=g, device=dev,
+                      dtype=torch.int32).to(torch.int16)
+    suh = (torch.randint(0, 2, (ic,), generator=g, device=dev) * 2 - 1).half()
+    svh = ((torch.randn(oc, generator=g, device=dev).abs() / math.sqrt(ic)).half()
+           * (torch.randint(0, 2, (oc,), generator=g, device=dev) * 2 - 1).half())
+    return dict(trellis=t, suh=suh, svh=svh, oc=oc, K=K, codebook=0)
+
+
+def _graph(dev, fn, settle=True):
+    """Capture fn() into a HIP graph on a side stream (one eager call first settles the
+    stream's persistent GEMV workspace outside the capture)."""
+    import torch
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        if settle:
+            fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            fn()
+    torch.cuda.synchronize()
+    return graph, side
+
+
+def _time_graph(graph, side, reps: int) -> float:
+    """Seconds per replay: one warm replay, then `reps` replays between HIP events recorded
+    on the replay stream."""
+    import torch
+    with torch.cuda.stream(side):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(side)
+    with torch.cuda.stream(side):
+        for _ in range(reps):
+            graph.replay()
+    e1.record(side)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def stack_bench(tokens: int = 20) -> dict:
+    """Config 4: the linear stack of a 64-layer Qwen-27B-shaped decoder at batch-1 decode,
+    one token = the int8 embedding gather, per layer the grouped q/k/v GEMV, o_proj, the
+    grouped gate/up GEMV and down_proj (K from the seeded {2,3,4,5} draw), then the K=6
+    lm_head.  Attention, norms and the activation function are excluded (BASELINE
+    config 4); each projection reads a fixed activation of its input width, which changes
+    no work.  The token is captured once into a HIP graph and replayed `tokens` times."""
+    import torch
+    from orcasaq2 import _native
+    from orcasaq2 import synthetic as syn
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(4)
+    shapes = syn.stack_shapes()
+    layers = []
+    nbytes = 0
+    for bits in syn.stack_bits():
+        L = {n: _rand_linear(*shapes[n], bits[n], g, dev) for n in shapes}
+        nbytes += sum(syn.packed_bytes(*shapes[n], bits[n]) for n in shapes)
+        layers.append(L)
+    head = _rand_linear(syn.HIDDEN, syn.VOCAB, 6, g, dev)
+    nbytes += syn.packed_bytes(syn.HIDDEN, syn.VOCAB, 6)
+    table = torch.randint(-128, 128, (syn.VOCAB, syn.HIDDEN), generator=g, device=dev, dtype=torch.int8)
+    scales = (torch.rand(syn.VOCAB, 1, generator=g, device=dev) * 0.02).half()
+    ids = torch.tensor([12345], device=dev)
+    nbytes += syn.HIDDEN + 2
+    xh = torch.randn(1, syn.HIDDEN, generator=g, device=dev).half()
+    xq = torch.randn(1, syn.Q_OUT, generator=g, device=dev).half()
+    xi = torch.randn(1, syn.INTERMEDIATE, generator=g, device=dev).half()
+    y_qkv = torch.empty(1, syn.Q_OUT + 2 * syn.KV_OUT, dtype=torch.half, device=dev)
+    y_gu = torch.empty(1, 2 * syn.INTERMEDIATE, dtype=torch.half, device=dev)
+    y_h = torch.empty(1, syn.HIDDEN, dtype=torch.half, device=dev)
+    logits = torch.empty(1, syn.VOCAB, dtype=torch.half, device=dev)
+
+    def token():
+        _native.embed_int8(table, scales, ids)
+        for L in layers:
+            _native.gemv_grouped(xh, [L["q"], L["k"], L["v"]], out=y_qkv)
+            _native.gemv_grouped(xq, [L["o"]], out=y_h)
+            _native.gemv_grouped(xh, [L["gate"], L["up"]], out=y_gu)
+            _native.gemv_grouped(xi, [L["down"]], out=y_h)
+        _native.gemv_grouped(xh, [head], out=logits)
+
+    graph, side = _graph(dev, token)
+    sec = _time_graph(graph, side, tokens)
+    del graph
+    return {"tok_s": round(1.0 / sec, 2), "ms_per_token": round(sec * 1e3, 4), "bytes_per_token": nbytes,
+            "GB/s": round(nbytes / sec / 1e9, 1), "frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
+            "tokens": tokens,
+            "what": "config4 measured: 64-layer Qwen-27B-shaped linear stack + K=6 lm_head + int8 embedding "
+                    "gather, batch 1, one HIP-graph-launched token replayed; attention/KV excluded"}
+
+
+def config2_bench(reps: int) -> dict:
+    """Config 2: grouped q/k/v (K 4/5/5) and gate/up (K 3/3) GEMVs at batch 1, 4 and 16,
+    each call on a different weight copy (> 512 MB rotated per projection group)."""
+    import torch
+    from orcasaq2 import _native
+    from orcasaq2 import synthetic as syn
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(2)
+    H = syn.HIDDEN
+    groups = {"qkv": [(syn.Q_OUT, 4), (syn.KV_OUT, 5), (syn.KV_OUT, 5)],
+              "gate_up": [(syn.INTERMEDIATE, 3), (syn.INTERMEDIATE, 3)]}
+    out = {}
+    for name, spec in groups.items():
+        gbytes = sum(syn.packed_bytes(H, oc, K) for oc, K in spec)
+        n = max(2, math.ceil(ROTATE_BYTES / gbytes))
+        copies = [[_rand_linear(H, oc, K, g, dev) for oc, K in spec] for _ in range(n)]
+        total = sum(oc for oc, _ in spec)
+        for rows in (1, 4, 16):
+            x = torch.randn(rows, H, generator=g, device=dev).half()
+            y = torch.empty(rows, total, dtype=torch.half, device=dev)
+
+            def run():
+                for c in copies:
+                    _native.gemv_grouped(x, c, out=y)
+
+            graph, side = _graph(dev, run)
+            sec = _time_graph(graph, side, max(1, reps // n)) / n
+            del graph
+            out[f"{name}_b{rows}"] = {"us_per_call": round(sec * 1e6, 3), "packed_bytes": gbytes,
+                                      "GB/s": round(gbytes / sec / 1e9, 1),
+                                      "frac": round(gbytes / sec / 1e9 / HBM_PEAK_GBS, 4)}
+        del copies
+    return out
+
+
+def config3_bench(reps: int) -> dict:
+    """Config 3: prefill GEMM of M=2048 rows through down_proj (17408 -> 5120, K=4), and a
+    standalone reconstruct of the same weight to fp16 (ic, oc)."""
+    import torch
+    from orcasaq2 import _native
+    from orcasaq2 import synthetic as syn
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(3)
+    ic, oc, K, M = syn.INTERMEDIATE, syn.HIDDEN, 4, 2048
+    lin = _rand_linear(ic, oc, K, g, dev)
+    x = torch.randn(M, ic, generator=g, device=dev).half()
+    y = torch.empty(M, oc, dtype=torch.half, device=dev)
+    W = torch.empty(ic, oc, dtype=torch.half, device=dev)
+
+    def gemm():
+        _native.gemm(x, lin["trellis"], lin["suh"], lin["svh"], K, 0, out=y)
+
+    def recon():
+        _native.reconstruct(lin["trellis"], K, 0, out=W)
+
+    gg, side = _graph(dev, gemm)
+    t_gemm = _time_graph(gg, side, reps)
+    gr, side_r = _graph(dev, recon)
+    t_rec = _time_graph(gr, side_r, reps)
+    flops = 2 * M * ic * oc
+    rbytes = syn.packed_bytes(ic, oc, K) + 2 * ic * oc
+    return {"gemm": {"us_per_call": round(t_gemm * 1e6, 2), "flop": flops,
+                     "TFLOP/s": round(flops / t_gemm / 1e12, 2),
+                     "mfma_util": round(flops / t_gemm / 1e12 / MFMA_F16_PEAK_TFS, 4),
+                     "peak_TFLOP/s": MFMA_F16_PEAK_TFS},
+            "reconstruct": {"us_per_call": round(t_rec * 1e6, 2), "bytes": rbytes,
+                            "GB/s": round(rbytes / t_rec / 1e9, 1),
+                            "frac": round(rbytes / t_rec / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
 def cpu_baseline(max_seconds: float = 30.0) -> dict:
@@ -230,6 +393,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-K", type=int, default=0, help="time a single K (profiling runs)")
     ap.add_argument("--copy-calib", action="store_true", help="run the counter-calibration copy and exit")
+    ap.add_argument("--workload", default="config1", choices=("config1", "config2", "config3"),
+                    help="config1 = the headline line (+ the config-4 stack); config2/config3 print "
+                         "their own measurement line")
+    ap.add_argument("--no-stack", action="store_true", help="skip the config-4 stack measurement")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the EXL3 linear path has no "
@@ -238,6 +405,12 @@ def main():
 
     if args.copy_calib:
         copy_calib(args)
+        return
+    if args.workload in ("config2", "config3"):
+        import torch
+        res = config2_bench(args.steps * 5) if args.workload == "config2" else config3_bench(args.steps)
+        print(json.dumps({"workload": args.workload, "results": res,
+                          "device": torch.cuda.get_device_name(0)}), flush=True)
         return
     r = gpu_bench(args)
     dom = r["per_k"][r["dom"]]
@@ -264,11 +437,12 @@ def main():
                      "bytes_per_launch": dom["bytes"], "mean_launch_us": round(dom["mean_us"], 3)},
         "per_K": {str(K): {"GB/s": round(v["gbs"], 1), "frac": round(v["frac"], 4),
                            "mean_us": round(v["mean_us"], 3)} for K, v in r["per_k"].items()},
-        "tok_s_equiv": round(r["value"] * 1e9 / r["tok_bytes"], 1),
-        "tok_s_equiv_note": "config-1 aggregate GB/s / config-4 packed bytes per token "
-                            f"({r['tok_bytes']} B); attention and KV excluded",
         "device": r["device"],
     }
+    if not args.no_stack and not args.only_K:
+        st = stack_bench()
+        out["tok_s_equiv"] = st["tok_s"]
+        out["stack"] = st
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

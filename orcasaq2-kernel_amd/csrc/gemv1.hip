@@ -7,31 +7,35 @@
 // Work decomposition.  A *unit* is one tile row of one 128-output column group: 8 tiles
 // side by side, 64 chunks of 32 positions -- one chunk per lane of a wave, the 8 tiles'
 // words one contiguous run of 64K u32 in HBM.  Units are numbered shard-major, then
-// column group, then tile row, and the whole launch's units are cut into G equal
+// column group, then tile row, and the whole launch's units are cut into G nearly equal
 // contiguous ranges, one per workgroup (G = a few workgroups per CU, all resident at
 // once: there is no tail wave of workgroups).  A workgroup's range touches a few
-// *segments* (shard, column group); its waves take the range's units round-robin.
+// *segments* (shard, column group); its waves take the range's units round-robin, so
+// the eight units a workgroup works on at once are the eight tile rows of one 128-input
+// block (segments start on block boundaries).
 //
 // Per workgroup:
-//   1. each wave issues the loads of its first D units (D = 2..6 by K, about 24 VGPRs of
-//      words in flight per lane), so HBM is busy from the start;
-//   2. main loop over the wave's units: a unit's K words (+ the tail-biting word before
-//      them) per lane stream through the D-deep register ring.  The tile row's 16
-//      activations fp16(H(x * suh)) are built in registers from the 128-input block (one
-//      x and one suh dword per lane; per-lane sign factor, cross-lane shuffles over lane
-//      bits 3..5, butterflies over lane bits 0..2), one unit ahead of its use.  Each
-//      position is decoded with an SDWA add (or a 16-bit field for MCG), a v_mul_lo_u32 and
-//      a v_bitop3; the masked word meets its activation in a v_dot2c_f32_f16 whose second
-//      operand is broadcast by DPP from the lane that owns the activation row (both fp16
-//      halves times x, summed in fp32);
-//   3. per segment, the waves' partial sums are added in a fixed order through LDS.  If the
+//   1. each wave issues the loads of its first D units (D = 2..6 by K), so HBM is busy
+//      from the start; only the trellis words are loaded per unit;
+//   2. the activations fp16(H128(x * suh)) of every block the range touches are built once
+//      (one block per wave: FWHT across the wave) into an LDS table holding, per unit, its
+//      tile row's 16 values as duplicated fp16 pairs;
+//   3. main loop over the wave's units: a unit's K words per lane stream through the
+//      D-deep register ring; the tail-biting word before a lane's chunk is the previous
+//      lane's last word (DPP rotate within the tile's 8 lanes).  Each position is decoded
+//      with an SDWA add (or a 16-bit field for MCG), a v_mul_lo_u32 and a v_bitop3; the
+//      masked word meets its activation in a v_dot2c_f32_f16 whose second operand is
+//      broadcast by DPP from the lane that holds that activation row (both fp16 halves
+//      times x, summed in fp32);
+//   4. per segment, the waves' partial sums are added in a fixed order through LDS.  If the
 //      segment lies inside this workgroup's range it is finished here; otherwise the
 //      partial goes to this workgroup's slot with agent-coherent stores, and the last of the
-//      segment's workgroups to arrive (a relaxed agent-scope counter in the workspace) adds
-//      all slots in slot order -- deterministic -- and finishes: output Hadamard, * svh,
-//      fp16 store, counter back to 0.  No cache-wide release/acquire is used: the slots
-//      are written with agent-scope stores and read with agent-scope loads, and each
-//      writer waits for its stores to complete before it increments the counter.
+//      segment's workgroups to arrive (a relaxed agent-scope counter in the workspace) has
+//      its eight waves add all slots (a fixed partition and order: deterministic) and
+//      finishes: output Hadamard, * svh, fp16 store, counter back to 0.  No cache-wide
+//      release/acquire is used: the slots are written with agent-scope stores and read
+//      with agent-scope loads, and each writer waits for its stores to complete before it
+//      increments the counter.
 #include "exl3_common.h"
 #include "exl3_launch.h"
 
@@ -43,15 +47,12 @@ constexpr int G1_WG_PER_CU = 4;          // target resident workgroups per CU (8
 constexpr int G1_GMAX = 2048;            // workgroups per launch (bounds the slot area)
 
 // Prefetch depth in units: about 24 VGPRs of loads in flight per lane whatever K is (a unit
-// is K + 1 trellis words plus an x and a suh word per lane), 2..6 units.
-template <int K>
-struct G1Depth {
-    static constexpr int value = (24 / (K + 3)) < 2 ? 2 : (24 / (K + 3)) > 6 ? 6 : (24 / (K + 3));
-};
+// is K trellis words and an activation pair per lane), 2..6 units.
+constexpr int g1_depth(int K) { return (24 / (K + 3)) < 2 ? 2 : (24 / (K + 3)) > 6 ? 6 : (24 / (K + 3)); }
 
 struct G1Shard {
     const uint32_t* trellis;   // (ic/16, oc/16, 8K) u32
-    const uint16_t* suh;       // (ic)
+    const uint32_t* act;       // (ic/16, 16) activation pairs of this shard (gemv1_act_kernel)
     const uint16_t* svh;       // (oc)
     uint16_t* C;               // (oc) fp16 output
     int ubeg;                  // first unit of the shard
@@ -60,136 +61,203 @@ struct G1Shard {
     int ncg;                   // column groups (oc / 128)
 };
 
+// Division by a launch constant d >= 2 of any x < 2^31 without a division routine (the
+// scalar unit is shared by every wave of a CU, and a 64-bit division is ~130 of its
+// instructions): floor(x / d) = floor(x * m / 2^(31 + l)), l = ceil(log2 d),
+// m = floor(2^(31 + l) / d) + 1 < 2^32 (Granlund and Montgomery, PLDI 1994, Thm 4.2 with
+// N = 31).
+struct G1Div {
+    uint32_t m;
+    int sh;                    // l - 1
+};
+
+__device__ __forceinline__ int g1_div(int x, G1Div d)
+{
+    return (int)(__umulhi((uint32_t)x, d.m) >> d.sh);
+}
+
 struct G1Args {
     const uint16_t* x;         // (ic) fp16
     uint32_t* counters;        // one per segment; zero between calls
     float* slots;              // (G + segments) x 128 fp32
     int U, G, ntr, nshards, nsegs;
+    int q, r;                  // U = q G + r: workgroup g owns q + (g < r) units
+    G1Div dntr, dq, dq1;       // division by ntr, q, q + 1
     G1Shard sh[G1_MAXSH];
 };
 
-// Workgroup whose unit range [floor(g U / G), floor((g+1) U / G)) holds unit u.
-__device__ __forceinline__ int g1_wg_of(int u, int U, int G)
+// First unit of workgroup g: the first r workgroups own q + 1 units, the others q.
+__device__ __forceinline__ int g1_first_unit(const G1Args& a, int g)
 {
-    return (int)((((long)u + 1) * G - 1) / U);
+    return g * a.q + min(g, a.r);
 }
 
+// Workgroup whose unit range holds unit u.
+__device__ __forceinline__ int g1_wg_of(const G1Args& a, int u)
+{
+    const int big = a.r * (a.q + 1);
+    return u < big ? g1_div(u, a.dq1) : a.r + g1_div(u - big, a.dq);
+}
+
+// Shard holding segment S / unit u.  Every table entry is read at a constant offset, so the
+// scalar loads of the whole table issue together instead of as a chain of dependent loads
+// (each a few hundred cycles); a single-shard launch (ONE) reads nothing.
+template <bool ONE>
 __device__ __forceinline__ int g1_shard_of_seg(const G1Args& a, int S)
 {
     int s = 0;
+    if constexpr (!ONE) {
 #pragma unroll
-    for (int i = 1; i < G1_MAXSH; i++)
-        if (i < a.nshards && S >= a.sh[i].sbeg) s = i;
+        for (int i = 1; i < G1_MAXSH; i++)
+            if (i < a.nshards && S >= a.sh[i].sbeg) s = i;
+    }
+    return s;
+}
+
+template <bool ONE>
+__device__ __forceinline__ int g1_shard_of_unit(const G1Args& a, int u)
+{
+    int s = 0;
+    if constexpr (!ONE) {
+#pragma unroll
+        for (int i = 1; i < G1_MAXSH; i++)
+            if (i < a.nshards && u >= a.sh[i].ubeg) s = i;
+    }
     return s;
 }
 
 __device__ __forceinline__ float g1_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu)); }
 __device__ __forceinline__ float g1_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
 
-// A lane's chunk: w[1..K] = its K words, w[0] = the tile's word before them (wrapping).
+// A lane's K words w[1..K] of a unit (lane l's chunk starts at word lk = K l), in the
+// widest loads their 4-byte alignment allows (dwordx4/x3/x2).
 template <int K>
-__device__ __forceinline__ void g1_load(uint32_t (&w)[K + 1], const uint32_t* __restrict__ unit, uint32_t lk,
-                                        uint32_t lprev)
+__device__ __forceinline__ void g1_load(uint32_t (&w)[K + 1], const uint32_t* __restrict__ unit, uint32_t lk)
 {
+    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
     const uint32_t* p = unit + lk;
-    if constexpr (K == 4) {
-        const uint4 v = *reinterpret_cast<const uint4*>(p);
-        w[1] = v.x; w[2] = v.y; w[3] = v.z; w[4] = v.w;
-    } else if constexpr (K == 8) {
-        const uint4 v = *reinterpret_cast<const uint4*>(p);
-        const uint4 u = *reinterpret_cast<const uint4*>(p + 4);
-        w[1] = v.x; w[2] = v.y; w[3] = v.z; w[4] = v.w;
-        w[5] = u.x; w[6] = u.y; w[7] = u.z; w[8] = u.w;
-    } else if constexpr (K == 2 || K == 6) {
+    int i = 0;
 #pragma unroll
-        for (int i = 0; i < K; i += 2) {
-            const uint2 v = *reinterpret_cast<const uint2*>(p + i);
-            w[i + 1] = v.x;
-            w[i + 2] = v.y;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < K; i++) w[i + 1] = p[i];
+    for (; i + 4 <= K; i += 4) {
+        uint4 v;
+        __builtin_memcpy(&v, p + i, 16);
+        w[i + 1] = v.x; w[i + 2] = v.y; w[i + 3] = v.z; w[i + 4] = v.w;
     }
-    w[0] = unit[lprev];
+    if constexpr (K % 4 == 3) {
+        u32x3 v;
+        __builtin_memcpy(&v, p + i, 12);
+        w[i + 1] = v.x; w[i + 2] = v.y; w[i + 3] = v.z;
+    } else if constexpr (K % 4 == 2) {
+        u32x2 v;
+        __builtin_memcpy(&v, p + i, 8);
+        w[i + 1] = v.x; w[i + 2] = v.y;
+    } else if constexpr (K % 4 == 1) {
+        w[i + 1] = p[i];
+    }
 }
+
+// w[0], the tile's word before the lane's chunk (tail-biting: the tile's last word for the
+// tile's first lane), is the last word w[K] of the previous lane within the tile's 8 lanes:
+// a rotate by one inside each 8-lane group, made of two 16-lane-row rotates (DPP row_ror:1
+// serves lanes 1..7 of a group, row_ror:9 lane 0).
+template <int K>
+__device__ __forceinline__ void g1_prev(uint32_t (&w)[K + 1], bool first_lane)
+{
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[K], 0x121, 0xf, 0xf, false);
+    const uint32_t r9 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[K], 0x129, 0xf, 0xf, false);
+    w[0] = first_lane ? r9 : r1;
+}
+
+__device__ __forceinline__ uint32_t g1_dup(float v)
+{
+    const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)v);
+    return h | (h << 16);
+}
+
+// ---------------------------------------------------------------- activation pass
+
+struct G1ActArgs {
+    const uint16_t* x;                 // (ic) fp16
+    int nsh, nblk;                     // shards, 128-input blocks per shard
+    const uint16_t* suh[G1_MAXSH];     // (ic) per shard
+    uint32_t* act[G1_MAXSH];           // (ic/16, 16) per shard
+};
+
+// fp16(H128(x * suh)) of every 128-input block, one wave per (shard, block), written as the
+// decode kernel reads it: tile row t of the block (16 inputs) is 16 dwords, dword r = fp16
+// value of row r duplicated in both halves.  Lane l ends the FWHT with outputs 2l, 2l + 1,
+// rows 2(l % 8), 2(l % 8) + 1 of tile row l / 8: one 8-byte store per lane.
+__global__ __launch_bounds__(256) void gemv1_act_kernel(const G1ActArgs a)
+{
+    const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (w >= a.nsh * a.nblk) return;   // whole waves only
+    const int s = w / a.nblk, b = w - s * a.nblk;
+    const uint32_t xw = reinterpret_cast<const uint32_t*>(a.x + b * 128)[lane];
+    const uint32_t sw = reinterpret_cast<const uint32_t*>(a.suh[s] + b * 128)[lane];
+    float v0 = g1_lo(xw) * g1_lo(sw), v1 = g1_hi(xw) * g1_hi(sw);
+    wave_fwht128(v0, v1);
+    *reinterpret_cast<uint2*>(a.act[s] + (8 * b + (lane >> 3)) * 16 + 2 * (lane & 7)) = uint2{g1_dup(v0), g1_dup(v1)};
+}
+
+// ---------------------------------------------------------------- decode kernel
 
 // Eight waves per SIMD need at most 64 VGPRs (measured on MI355X: 68 VGPRs leave room for
 // only 6); the SGPR cap keeps the count well inside what eight waves per SIMD may hold.
-template <int K, int CB>
+template <int K, int CB, bool ONE>
 __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8), amdgpu_num_sgpr(74))) void gemv1_kernel(const G1Args a)
 {
+    // shard table entry; a single-shard launch (ONE) only ever reads entry 0 (constant offsets)
+    auto sh = [&](int s) -> const G1Shard& { return a.sh[ONE ? 0 : s]; };
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    constexpr int D = g1_depth(K);
 
     const int g = blockIdx.x;
-    const int U = a.U, G = a.G, ntr = a.ntr, ntrb = ntr >> 3;
-    const int ub = (int)((long)g * U / G), ue = (int)((long)(g + 1) * U / G);
+    const int ntr = a.ntr;
+    const int ub = g1_first_unit(a, g), L = a.q + (g < a.r ? 1 : 0);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
 
-    // ---- this workgroup's segments: S_first .. S_first + nseg - 1
-    const int s_first = [&] {
-        int s = 0;
-#pragma unroll
-        for (int i = 1; i < G1_MAXSH; i++)
-            if (i < a.nshards && ub >= a.sh[i].ubeg) s = i;
-        return s;
-    }();
-    const int rel0 = ub - a.sh[s_first].ubeg;
-    const int S_first = a.sh[s_first].sbeg + rel0 / ntr;
-    const int t_first = rel0 % ntr;
-    const int nseg = [&] {
-        const int u = ue - 1;
-        int s = 0;
-#pragma unroll
-        for (int i = 1; i < G1_MAXSH; i++)
-            if (i < a.nshards && u >= a.sh[i].ubeg) s = i;
-        return a.sh[s].sbeg + (u - a.sh[s].ubeg) / ntr - S_first + 1;
-    }();
-    float* red = reinterpret_cast<float*>(lds);                // [nseg][G1_NW][128]
-
     // ---- this wave's units: ub + wave + G1_NW * j, j < n
-    const int n = (ue - ub > wave) ? (ue - ub - wave + G1_NW - 1) / G1_NW : 0;
-    const int c = lane & 7;
+    const int n = (L > wave) ? (L - wave + G1_NW - 1) / G1_NW : 0;
     const uint32_t lk = lane * K;
-    const uint32_t lprev = c ? lk - 1 : lk + 8 * K - 1;
+    const uint32_t la = 2 * (lane & 7);       // the lane's two activation rows in a tile row
+    const bool first_lane = (lane & 7) == 0;
 
-    // Wave-uniform cursor over the wave's units: shard, column group, tile row, segment
-    // index within the workgroup, the first word of the unit's 8 tiles and the shard's
-    // suh.  Consecutive units of a wave are G1_NW tile rows apart (ntr >= 8, so a step
-    // crosses at most one column-group boundary); only such a crossing reads the shard
-    // table again.
+    // Wave-uniform cursor over the wave's units: shard, column group, tile row, segment, the
+    // first word of the unit's 8 tiles and the unit's activation row.  Consecutive units of
+    // a wave are G1_NW tile rows apart (ntr >= 8, so a step crosses at most one
+    // column-group boundary); only such a crossing reads the shard table again.
     struct Cursor {
-        int s, cg, tr, k;
+        int s, cg, tr, S;
         long stride;   // words between tile rows G1_NW apart
         const uint32_t* p;
-        const uint16_t* suh;
+        const uint32_t* ap;
     };
     auto seat = [&](Cursor& q) {
-        q.stride = (long)G1_NW * a.sh[q.s].oc16 * (8 * K);
-        q.p = a.sh[q.s].trellis + ((long)q.tr * a.sh[q.s].oc16 + 8 * q.cg) * (8 * K);
-        q.suh = a.sh[q.s].suh;
+        q.stride = (long)G1_NW * sh(q.s).oc16 * (8 * K);
+        q.p = sh(q.s).trellis + ((long)q.tr * sh(q.s).oc16 + 8 * q.cg) * (8 * K);
+        q.ap = sh(q.s).act + q.tr * 16;
     };
     auto cursor_at = [&](int u) {
         Cursor q;
-        q.s = 0;
-#pragma unroll
-        for (int i = 1; i < G1_MAXSH; i++)
-            if (i < a.nshards && u >= a.sh[i].ubeg) q.s = i;
-        const int rel = u - a.sh[q.s].ubeg;
-        q.cg = rel / ntr;
+        q.s = g1_shard_of_unit<ONE>(a, u);
+        const int rel = u - sh(q.s).ubeg;
+        q.cg = g1_div(rel, a.dntr);
         q.tr = rel - q.cg * ntr;
-        q.k = a.sh[q.s].sbeg + q.cg - S_first;
+        q.S = sh(q.s).sbeg + q.cg;
         seat(q);
         return q;
     };
     auto advance = [&](Cursor& q) {
         q.tr += G1_NW;
         q.p += q.stride;
+        q.ap += G1_NW * 16;
         if (q.tr >= ntr) {
             q.tr -= ntr;
-            q.k++;
-            if (++q.cg == a.sh[q.s].ncg) {
+            q.S++;
+            if (++q.cg == sh(q.s).ncg) {
                 q.s++;
                 q.cg = 0;
             }
@@ -197,22 +265,17 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
         }
     };
 
-    // A unit's loads: the lane's K words + the tail-biting word, and the 128 inputs (x and
-    // suh, one dword each per lane) of the tile row's Hadamard block.
-    constexpr int D = G1Depth<K>::value;
+    // A unit's loads: the lane's K words and its activation pair.  Prefetch cursor (D units
+    // ahead; it stops at the wave's last unit, whose data is then loaded again and not used)
+    // and processing cursor.
     struct Slot {
         uint32_t w[K + 1];
-        uint32_t xw, sw;
+        uint2 av;
     };
     auto load = [&](Slot& sl, const Cursor& q) {
-        g1_load<K>(sl.w, q.p, lk, lprev);
-        const int blk = q.tr >> 3;
-        sl.xw = reinterpret_cast<const uint32_t*>(a.x + blk * 128)[lane];
-        sl.sw = reinterpret_cast<const uint32_t*>(q.suh + blk * 128)[lane];
+        g1_load<K>(sl.w, q.p, lk);
+        sl.av = *reinterpret_cast<const uint2*>(q.ap + la);
     };
-
-    // prefetch cursor (D units ahead; it stops at the wave's last unit, whose data is then
-    // loaded again and not used) and processing cursor
     Cursor pf = cursor_at(ub + wave), cu = pf;
     int jpf = 0;
     auto next_pf = [&]() -> const Cursor& {
@@ -228,43 +291,45 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
 #pragma unroll
         for (int d = 1; d < D; d++) load(ring[d], next_pf());
     }
+
+    // ---- this workgroup's segments: S_first .. S_first + nseg - 1
+    const int s_first = g1_shard_of_unit<ONE>(a, ub);
+    const int S_first = sh(s_first).sbeg + g1_div(ub - sh(s_first).ubeg, a.dntr);
+    const int nseg = [&] {
+        const int u = ub + L - 1;
+        const int s = g1_shard_of_unit<ONE>(a, u);
+        return sh(s).sbeg + g1_div(u - sh(s).ubeg, a.dntr) - S_first + 1;
+    }();
+    // LDS: red[nseg][G1_NW][128] fp32 partial rows | last[nseg] flags
+    float* red = reinterpret_cast<float*>(lds);
+    int* last = reinterpret_cast<int*>(red + nseg * G1_NW * 128);
     for (int k = 0; k < nseg; k++)
         *reinterpret_cast<float2*>(red + (k * G1_NW + wave) * 128 + 2 * lane) = float2{0.f, 0.f};
     const Dot2Consts kc = dot2_consts();
-    // A wave's units are G1_NW = 8 tile rows apart and segments start on 128-input block
-    // boundaries, so its tile row within the block -- and the activation signs -- never change.
-    const float fact = tile_row_factor(cu.tr & 7, lane);
 
     // ---- main loop.  Scalar bookkeeping (cursor steps, column-group crossings, flushes of a
-    // finished segment's sums to the wave's LDS row) sits between units, so each unit's
-    // work is one basic block the scheduler can interleave; the loads sit outside every
-    // branch, so the wait before a unit covers only that unit's own loads.
-    const int o0 = (lane >> 3) * 16 + c;
+    // finished segment's sums to the wave's LDS row) sits between units, so each unit's work
+    // is one basic block the scheduler can interleave; the loads sit outside every branch,
+    // so the wait before a unit covers only that unit's own loads.
+    const int o0 = (lane >> 3) * 16 + (lane & 7);
     float y0 = 0.f, y1 = 0.f;
-    int cur = 0;
+    int cur = cu.S - S_first;
     auto flush = [&](int k) {
         red[(cur * G1_NW + wave) * 128 + o0] = y0;
         red[(cur * G1_NW + wave) * 128 + o0 + 8] = y1;
         y0 = y1 = 0.f;
         cur = k;
     };
-    // The activations of unit j + 1 are built while unit j decodes (their cross-lane
-    // shuffles wait on LDS; the decode hides that).
-    uint32_t a0 = 0, a1 = 0;
-    if (n > 0) tile_row_act(ring[0].xw, ring[0].sw, fact, lane, a0, a1);
     for (int j = 0; j < n; j += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
             if (d == 0 || j + d < n) {
-                if (cu.k != cur) flush(cu.k);
-                uint32_t b0, b1;
-                tile_row_act(ring[(d + 1) % D].xw, ring[(d + 1) % D].sw, fact, lane, b0, b1);
+                if (cu.S - S_first != cur) flush(cu.S - S_first);
+                g1_prev<K>(ring[d].w, first_lane);
                 float acc[4] = {0.f, 0.f, 0.f, 0.f};
-                dot2_chunk<K, CB>(ring[d].w, a0, a1, acc, kc);
+                dot2_chunk<K, CB>(ring[d].w, ring[d].av.x, ring[d].av.y, acc, kc);
                 y0 += acc[0] + acc[1];
                 y1 += acc[2] + acc[3];
-                a0 = b0;
-                a1 = b1;
                 if (j + d + 1 < n) advance(cu);
             }
             load(ring[d], next_pf());
@@ -273,7 +338,27 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     if (n > 0) flush(cur);
     __syncthreads();
 
-    // ---- per segment: fixed-order sum of the waves, then finish here or via the slots
+    // ---- per segment: fixed-order sum of the waves; finish here, or via the slots
+    auto finish = [&](int k, float v0, float v1) {
+        const int S = S_first + k;
+        const int s = g1_shard_of_seg<ONE>(a, S);
+        const int cg = S - sh(s).sbeg;
+        wave_fwht128(v0, v1);
+        const uint32_t sv = reinterpret_cast<const uint32_t*>(sh(s).svh + cg * 128)[lane];
+        v0 *= g1_lo(sv);
+        v1 *= g1_hi(sv);
+        const uint32_t out = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) |
+                             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
+        reinterpret_cast<uint32_t*>(sh(s).C + cg * 128)[lane] = out;
+    };
+    auto contributors = [&](int k, int& g_lo, int& g_hi) {
+        const int S = S_first + k;
+        const int s = g1_shard_of_seg<ONE>(a, S);
+        const int segU0 = sh(s).ubeg + (S - sh(s).sbeg) * ntr;
+        g_lo = g1_wg_of(a, segU0);
+        g_hi = g1_wg_of(a, segU0 + ntr - 1);
+    };
+    bool any_last = false;
     for (int k = wave; k < nseg; k += G1_NW) {
         float v0 = 0.f, v1 = 0.f;
 #pragma unroll
@@ -282,62 +367,85 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
             v0 += p.x;
             v1 += p.y;
         }
-        const int S = S_first + k;
-        const int s = g1_shard_of_seg(a, S);
-        const int cg = S - a.sh[s].sbeg;
-        const int segU0 = a.sh[s].ubeg + cg * ntr;
-        const int g_lo = g1_wg_of(segU0, U, G), g_hi = g1_wg_of(segU0 + ntr - 1, U, G);
+        int g_lo, g_hi;
+        contributors(k, g_lo, g_hi);
+        int is_last = 0;
         if (g_hi > g_lo) {
-            float* my = a.slots + (long)(S + g) * 128 + 2 * lane;
-            __hip_atomic_store(my, v0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(my + 1, v1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + (long)(S_first + k + g) * 128) + lane;
+            const uint64_t pv = (uint64_t)__builtin_bit_cast(uint32_t, v0) |
+                                ((uint64_t)__builtin_bit_cast(uint32_t, v1) << 32);
+            __hip_atomic_store(my, pv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __builtin_amdgcn_s_waitcnt(0);   // this wave's slot stores are complete
             uint32_t old = 0;
             if (lane == 0)
-                old = __hip_atomic_fetch_add(a.counters + S, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                old = __hip_atomic_fetch_add(a.counters + S_first + k, 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
             old = __shfl(old, 0, 64);
-            if (old != (uint32_t)(g_hi - g_lo)) continue;
             // last to arrive: every other contributor's slot stores completed before its
             // counter increment, which precedes ours
-            v0 = v1 = 0.f;
-            const float* sl = a.slots + (long)(S + g_lo) * 128 + 2 * lane;
+            is_last = old == (uint32_t)(g_hi - g_lo);
+            if (is_last && lane == 0)
+                __hip_atomic_store(a.counters + S_first + k, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            finish(k, v0, v1);
+        }
+        if (lane == 0) last[k] = is_last;
+        any_last |= is_last != 0;
+    }
+    // Segments this workgroup completes for everyone: the eight waves add the slots (wave w
+    // takes slots g_lo + w, g_lo + w + 8, ... in order), then wave k adds the eight sums.
+    if (__syncthreads_or(any_last)) {
+        for (int k = 0; k < nseg; k++) {
+            if (!last[k]) continue;
+            int g_lo, g_hi;
+            contributors(k, g_lo, g_hi);
             const int nsl = g_hi - g_lo + 1;
-            for (int g0 = 0; g0 < nsl; g0 += 16) {
-                float x0[16], x1[16];
+            const uint64_t* sl = reinterpret_cast<const uint64_t*>(a.slots + (long)(S_first + k + g_lo) * 128) + lane;
+            float v0 = 0.f, v1 = 0.f;
+            for (int t0 = wave; t0 < nsl; t0 += 8 * G1_NW) {
+                uint64_t xv[8];
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    const int gg = min(g0 + i, nsl - 1);
-                    x0[i] = __hip_atomic_load(sl + gg * 128, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    x1[i] = __hip_atomic_load(sl + gg * 128 + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int t = 0; t < 8; t++) {
+                    const int gg = min(t0 + t * G1_NW, nsl - 1);
+                    xv[t] = __hip_atomic_load(sl + (long)gg * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 }
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    if (g0 + i < nsl) {
-                        v0 += x0[i];
-                        v1 += x1[i];
+                for (int t = 0; t < 8; t++) {
+                    if (t0 + t * G1_NW < nsl) {
+                        v0 += __builtin_bit_cast(float, (uint32_t)xv[t]);
+                        v1 += __builtin_bit_cast(float, (uint32_t)(xv[t] >> 32));
                     }
                 }
             }
-            if (lane == 0) __hip_atomic_store(a.counters + S, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *reinterpret_cast<float2*>(red + (k * G1_NW + wave) * 128 + 2 * lane) = float2{v0, v1};
         }
-        wave_fwht128(v0, v1);
-        const uint32_t sv = reinterpret_cast<const uint32_t*>(a.sh[s].svh + cg * 128)[lane];
-        v0 *= g1_lo(sv);
-        v1 *= g1_hi(sv);
-        const uint32_t out = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) |
-                             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
-        reinterpret_cast<uint32_t*>(a.sh[s].C + cg * 128)[lane] = out;
+        __syncthreads();
+        for (int k = wave; k < nseg; k += G1_NW) {
+            if (!last[k]) continue;
+            float v0 = 0.f, v1 = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < G1_NW; ww++) {
+                const float2 p = *reinterpret_cast<const float2*>(red + (k * G1_NW + ww) * 128 + 2 * lane);
+                v0 += p.x;
+                v1 += p.y;
+            }
+            finish(k, v0, v1);
+        }
     }
 }
 
 // ---------------------------------------------------------------- host side
 
 template <int K, int CB>
-static const void* g1_fn() { return reinterpret_cast<const void*>(&gemv1_kernel<K, CB>); }
-
-static const void* g1_fn_kcb(int K, int cb)
+static const void* g1_fn(bool one)
 {
-#define EXL3_CASE(KK) case KK: return cb == CB_MCG ? g1_fn<KK, CB_MCG>() : g1_fn<KK, CB_3INST>();
+    return one ? reinterpret_cast<const void*>(&gemv1_kernel<K, CB, true>)
+               : reinterpret_cast<const void*>(&gemv1_kernel<K, CB, false>);
+}
+
+static const void* g1_fn_kcb(int K, int cb, bool one)
+{
+#define EXL3_CASE(KK) case KK: return cb == CB_MCG ? g1_fn<KK, CB_MCG>(one) : g1_fn<KK, CB_3INST>(one);
     switch (K) {
         EXL3_CASE(1) EXL3_CASE(2) EXL3_CASE(3) EXL3_CASE(4)
         EXL3_CASE(5) EXL3_CASE(6) EXL3_CASE(7) EXL3_CASE(8)
@@ -361,21 +469,28 @@ static int g1_cu_count()
     return cus;
 }
 
-// Dynamic LDS a launch needs: a partial row per wave for the most segments (shard, column
-// group) a workgroup range of ceil(U / G) units can touch.
+static G1Div g1_magic(uint32_t d)
+{
+    int l = 0;
+    while ((1ull << l) < d) l++;
+    return G1Div{(uint32_t)(((1ull << (31 + l)) / d) + 1), l - 1};
+}
+
+// Dynamic LDS a launch needs: a partial row per wave and a flag for the most segments
+// (shard, column group) a workgroup range of ceil(U / G) units can touch.
 static size_t g1_lds_bytes(int U, int G, int ntr)
 {
     const int L = (U + G - 1) / G;
     const int nseg = (L - 1 + ntr - 1) / ntr + 1;
-    return (size_t)nseg * G1_NW * 128 * sizeof(float);
+    return (size_t)nseg * (G1_NW * 128 * sizeof(float) + 4);
 }
 
 // Per-shard share of the workspace after the counter area: slot rows for up to G1_GMAX
-// workgroups and one per column group.
+// workgroups and one per column group, the shard's activation pairs (4 bytes per input) and
+// alignment slack.
 size_t gemv1_slot_bytes(int ic, int oc)
 {
-    (void)ic;
-    return (size_t)(G1_GMAX + oc / 128) * 128 * sizeof(float);
+    return (size_t)(G1_GMAX + oc / 128) * 128 * sizeof(float) + (size_t)ic * 4 + 256;
 }
 
 int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint32_t* counters, int max_counters,
@@ -383,9 +498,32 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint
 {
     const int ic = shards[0].ic;
     const int ntr = ic / 16;
+
+    // Workspace after the counter area: the activation pairs of every shard (ic 4-byte
+    // entries each), then per launch its slot rows.  One activation pass serves all shards.
+    const size_t act_bytes = ((size_t)nshards * ic * 4 + 255) & ~(size_t)255;
+    if (act_bytes > slot_bytes)
+        return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: slot area of %zu bytes, %zu needed", slot_bytes, act_bytes);
+    auto act_of = [&](int s) { return reinterpret_cast<uint32_t*>(slots + (size_t)s * ic * 4); };
+    for (int s0 = 0; s0 < nshards; s0 += G1_MAXSH) {
+        G1ActArgs aa = {};
+        aa.x = A;
+        aa.nsh = std::min(G1_MAXSH, nshards - s0);
+        aa.nblk = ic / 128;
+        for (int k = 0; k < aa.nsh; k++) {
+            aa.suh[k] = shards[s0 + k].suh;
+            aa.act[k] = act_of(s0 + k);
+        }
+        void* akargs[] = {&aa};
+        hipLaunchKernel(reinterpret_cast<const void*>(&gemv1_act_kernel), dim3((aa.nsh * aa.nblk + 3) / 4),
+                        dim3(256), akargs, 0, stream);
+        const int rc = check_launch("exl3_gemv (batch 1 activations)");
+        if (rc != EXL3_OK) return rc;
+    }
+
     bool done[EXL3_MAX_SHARDS] = {false};
     int cbase = 0;
-    size_t sbase = 0;
+    size_t sbase = act_bytes;
     const int gmax = std::min(G1_GMAX, G1_WG_PER_CU * g1_cu_count());
     for (int i = 0; i < nshards; i++) {
         if (done[i]) continue;
@@ -399,7 +537,7 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint
             const GemvShard& d = shards[s];
             G1Shard& e = args.sh[args.nshards++];
             e.trellis = d.trellis;
-            e.suh = d.suh;
+            e.act = act_of(s);
             e.svh = d.svh;
             e.C = d.C;
             e.ubeg = (int)U;
@@ -415,7 +553,7 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint
         if (cbase + nsegs > max_counters)
             return set_error(EXL3_ERR_ARG, "exl3_gemv: %d column groups exceed the %d segment counters",
                              cbase + nsegs, max_counters);
-        int G = (int)std::min<long>(gmax, std::max<long>(1, U / G1_NW));
+        const int G = (int)std::min<long>(gmax, std::max<long>(1, U / G1_NW));
         const size_t lds = g1_lds_bytes((int)U, G, ntr);
         const size_t need = (size_t)(G + nsegs) * 128 * sizeof(float);
         if (sbase + need > slot_bytes)
@@ -423,12 +561,18 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint
                              sbase + need);
         args.U = (int)U;
         args.G = G;
+        args.q = (int)(U / G);
+        args.r = (int)(U % G);
+        // divisors are >= 8 (ntr = ic / 16 with ic >= 128; G <= U / 8), as g1_div requires
+        args.dntr = g1_magic((uint32_t)ntr);
+        args.dq = g1_magic((uint32_t)args.q);
+        args.dq1 = g1_magic((uint32_t)args.q + 1);
         args.nsegs = nsegs;
         args.counters = counters + cbase;
         args.slots = reinterpret_cast<float*>(slots + sbase);
         cbase += nsegs;
         sbase += need;
-        const void* fn = g1_fn_kcb(shards[i].K, shards[i].cb);
+        const void* fn = g1_fn_kcb(shards[i].K, shards[i].cb, args.nshards == 1);
         if (!fn) return set_error(EXL3_ERR_ARG, "exl3_gemv: K=%d is not in 1..8", shards[i].K);
         if (lds > 64 * 1024) {
             hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

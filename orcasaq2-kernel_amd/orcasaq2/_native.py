@@ -152,6 +152,7 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
 
 _gemv_ws: dict = {}
+_gemv_ws_retired: list = []
 
 
 def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
@@ -159,11 +160,15 @@ def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     zero in its counter area by every call (exl3hip.h), so it persists across calls and is
     reused -- also by HIP-graph replays of captured calls.  Calls on one stream run in
     order, so they can share it; another stream gets its own.  A call needing more gets a
-    larger zeroed buffer; the old one is released in stream order."""
+    larger zeroed buffer; the old one is released in stream order -- except during a graph
+    capture, where nodes already captured still point at it: it is then kept alive for the
+    life of the process."""
     stream = torch.cuda.current_stream(device).cuda_stream
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _gemv_ws.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None and torch.cuda.is_current_stream_capturing():
+            _gemv_ws_retired.append(ws)
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _gemv_ws[key] = ws
     return ws
