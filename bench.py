@@ -318,16 +318,37 @@ def config3_bench(reps: int) -> dict:
     def recon():
         _native.reconstruct(lin["trellis"], K, 0, out=W)
 
+    def op():
+        # the plugin's path for M > GEMM_MAX_ROWS: had_r_128 -> reconstruct -> library fp16
+        # GEMM -> had_r_128 (orcasaq2/ops.py:50-59 of the reference)
+        torch.ops.orcasaq2.shard_gemm(x, lin["trellis"], lin["suh"], lin["svh"], oc, float(K), False, False)
+
+    import orcasaq2.ops  # noqa: F401  (registers torch.ops.orcasaq2)
     gg, side = _graph(dev, gemm)
     t_gemm = _time_graph(gg, side, reps)
     gr, side_r = _graph(dev, recon)
     t_rec = _time_graph(gr, side_r, reps)
+    op()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        op()
+    e1.record()
+    torch.cuda.synchronize()
+    t_op = e0.elapsed_time(e1) * 1e-3 / reps
     flops = 2 * M * ic * oc
     rbytes = syn.packed_bytes(ic, oc, K) + 2 * ic * oc
     return {"gemm": {"us_per_call": round(t_gemm * 1e6, 2), "flop": flops,
                      "TFLOP/s": round(flops / t_gemm / 1e12, 2),
                      "mfma_util": round(flops / t_gemm / 1e12 / MFMA_F16_PEAK_TFS, 4),
-                     "peak_TFLOP/s": MFMA_F16_PEAK_TFS},
+                     "peak_TFLOP/s": MFMA_F16_PEAK_TFS,
+                     "what": "exl3_gemm: had_r_128 pass + fused decode-into-MFMA kernel"},
+            "op_reconstruct_branch": {"us_per_call": round(t_op * 1e6, 2),
+                                      "TFLOP/s": round(flops / t_op / 1e12, 2),
+                                      "mfma_util": round(flops / t_op / 1e12 / MFMA_F16_PEAK_TFS, 4),
+                                      "what": "torch.ops.orcasaq2.shard_gemm at M=2048 (eager): had_r_128, "
+                                              "reconstruct, library fp16 GEMM, had_r_128"},
             "reconstruct": {"us_per_call": round(t_rec * 1e6, 2), "bytes": rbytes,
                             "GB/s": round(rbytes / t_rec / 1e9, 1),
                             "frac": round(rbytes / t_rec / 1e9 / HBM_PEAK_GBS, 4)}}

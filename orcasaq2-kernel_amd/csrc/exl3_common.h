@@ -393,6 +393,19 @@ __device__ __forceinline__ void dot2_chunk(const uint32_t (&w)[K + 1], uint32_t 
     dot2_chunk_seq<K, CB>(w, d0, d1, acc, k, std::make_integer_sequence<int, 8>{});
 }
 
+// w[0] of a chunk -- the tile's word before the lane's chunk (tail-biting: the tile's last
+// word for the tile's first chunk) -- is the last word w[K] of the previous chunk of the
+// same tile, held by the previous lane when a tile's 8 chunks sit on 8 consecutive lanes
+// (aligned to 8): a rotate by one inside each 8-lane group, made of two 16-lane-row
+// rotates (DPP row_ror:1 serves lanes 1..7 of a group, row_ror:9 lane 0).
+template <int K>
+__device__ __forceinline__ void chunk_prev_dpp(uint32_t (&w)[K + 1], bool first_lane)
+{
+    const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[K], 0x121, 0xf, 0xf, false);
+    const uint32_t r9 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[K], 0x129, 0xf, 0xf, false);
+    w[0] = first_lane ? r9 : r1;
+}
+
 // ---------------------------------------------------------------- wave helpers
 
 // In-wave normalised Walsh-Hadamard of one 128-vector held as v0 = x[2l], v1 = x[2l+1]

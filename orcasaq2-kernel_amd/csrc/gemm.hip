@@ -1,4 +1,4 @@
-// Prefill EXL3 GEMM for more than 16 activation rows:
+// Prefill EXL3 GEMM for 17 to GEMM_SK_MIN_ROWS activation rows (more rows: gemm_sk.hip):
 //   C = fp16( H( fp16(H(A * suh)) . W_q ) * svh )
 // Replaces the reconstruct branch of orcasaq2/ops.py:50-59 (had_r_128 -> reconstruct ->
 // hgemm_recon -> had_r_128) with: one had_r_128 pass over A into the workspace, then one
@@ -21,10 +21,16 @@ constexpr int GM_KSTEP = 64;                 // inputs per step (4 tile rows)
 constexpr int GM_ASTRIDE = GM_KSTEP + 8;     // halves per staged activation row
 constexpr int GM_CSTRIDE = 128 + 4;          // floats per staged output row
 
+// Row counts above this take the stream-K kernel (gemm_sk.hip), which decodes each weight
+// once per 256 rows; at or below it, this kernel (one decode per 64 rows, no partial sums).
+constexpr int GEMM_SK_MIN_ROWS = 192;
+
+static size_t gemm_ah_bytes(int rows, int ic) { return ((size_t)rows * ic * sizeof(uint16_t) + 255) & ~(size_t)255; }
+
 size_t gemm_workspace_bytes(int rows, int ic, int oc)
 {
-    (void)oc;
-    return ((size_t)rows * ic * sizeof(uint16_t) + 255) & ~(size_t)255;
+    const size_t ah = gemm_ah_bytes(rows, ic);
+    return rows > GEMM_SK_MIN_ROWS ? ah + gemm_sk_slot_bytes(rows, oc, gemm_sk_cus()) : ah;
 }
 
 template <int K, int CB>
@@ -126,6 +132,11 @@ int gemm_dispatch(const uint16_t* A, const uint32_t* trellis, uint16_t* C, const
     uint16_t* Ah = static_cast<uint16_t*>(workspace);
     int rc = had_dispatch(A, Ah, suh, nullptr, 1.0f, rows, ic, stream);
     if (rc != EXL3_OK) return rc;
+    if (rows > GEMM_SK_MIN_ROWS) {
+        const size_t ah = gemm_ah_bytes(rows, ic);
+        return gemm_sk_dispatch(Ah, trellis, C, svh, static_cast<char*>(workspace) + ah, ws_bytes - ah, rows, ic, oc,
+                                K, cb, gemm_sk_cus(), stream);
+    }
 #define EXL3_CASE(KK)                                                                        \
     case KK:                                                                                 \
         if (cb == CB_MCG) launch_gemm<KK, CB_MCG>(Ah, trellis, C, svh, rows, ic, oc, stream); \

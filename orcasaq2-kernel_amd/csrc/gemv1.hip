@@ -157,18 +157,6 @@ __device__ __forceinline__ void g1_load(uint32_t (&w)[K + 1], const uint32_t* __
     }
 }
 
-// w[0], the tile's word before the lane's chunk (tail-biting: the tile's last word for the
-// tile's first lane), is the last word w[K] of the previous lane within the tile's 8 lanes:
-// a rotate by one inside each 8-lane group, made of two 16-lane-row rotates (DPP row_ror:1
-// serves lanes 1..7 of a group, row_ror:9 lane 0).
-template <int K>
-__device__ __forceinline__ void g1_prev(uint32_t (&w)[K + 1], bool first_lane)
-{
-    const uint32_t r1 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[K], 0x121, 0xf, 0xf, false);
-    const uint32_t r9 = (uint32_t)__builtin_amdgcn_mov_dpp((int)w[K], 0x129, 0xf, 0xf, false);
-    w[0] = first_lane ? r9 : r1;
-}
-
 __device__ __forceinline__ uint32_t g1_dup(float v)
 {
     const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)v);
@@ -325,7 +313,7 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
         for (int d = 0; d < D; d++) {
             if (d == 0 || j + d < n) {
                 if (cu.S - S_first != cur) flush(cu.S - S_first);
-                g1_prev<K>(ring[d].w, first_lane);
+                chunk_prev_dpp<K>(ring[d].w, first_lane);
                 float acc[4] = {0.f, 0.f, 0.f, 0.f};
                 dot2_chunk<K, CB>(ring[d].w, ring[d].av.x, ring[d].av.y, acc, kc);
                 y0 += acc[0] + acc[1];

@@ -80,6 +80,19 @@ def test_had_r_128(native, oracle, pre, post, scale):
     assert (err <= np.abs(ref) * 2.0 ** -10 + 2.0 ** -24).all()
 
 
+def test_had_r_128_4byte_aligned_pointers(native, oracle):
+    """pointers that are 4- but not 16-byte aligned take the narrow kernel"""
+    g = torch.Generator().manual_seed(7)
+    buf = torch.randn(5 * 384 + 2, generator=g).half().to(dev())
+    xv = buf[2:].view(5, 384)
+    assert xv.data_ptr() % 16 == 4
+    p = syn.signs(384, g)
+    y = native.had_r_128(xv, pre=p.to(dev()))
+    ref = oracle.had_r_128(xv.cpu().numpy(), p.numpy())
+    err = np.abs(f16(y).astype(np.float64) - ref)
+    assert (err <= np.abs(ref) * 2.0 ** -10 + 2.0 ** -24).all()
+
+
 def test_had_r_128_in_place(native, oracle):
     g = torch.Generator().manual_seed(6)
     x = torch.randn(3, 256, generator=g).half()
@@ -168,6 +181,26 @@ def test_gemm_K(native, oracle, K, cb):
     d = to_gpu(lin)
     y = native.gemm(x.to(dev()), d["trellis"], d["suh"], d["svh"], K, cb)
     check_linear_out(y, x, lin, cb, oracle)
+
+
+@pytest.mark.parametrize("rows,ic,oc,K,cb", [(257, 128, 128, 3, 0), (300, 640, 640, 4, 1), (520, 1024, 384, 2, 0),
+                                          (700, 256, 1152, 5, 0), (450, 384, 256, 8, 0)])
+def test_gemm_streamk_shapes(native, oracle, rows, ic, oc, K, cb):
+    """above 192 rows: 256 x 256 tiles split over workgroups by K-steps (ragged rows, output
+    counts that leave half a tile, tiny ic, both codebooks)"""
+    lin = syn.linear(ic, oc, K, seed=rows + oc)
+    x = syn.activations(rows, ic, torch.Generator().manual_seed(rows))
+    d = to_gpu(lin)
+    y = native.gemm(x.to(dev()), d["trellis"], d["suh"], d["svh"], K, cb)
+    check_linear_out(y, x, lin, cb, oracle)
+
+
+def test_gemm_streamk_deterministic(native):
+    lin = to_gpu(syn.linear(2048, 512, 4, seed=5))
+    x = syn.activations(600, 2048, torch.Generator().manual_seed(4)).to(dev())
+    ys = [native.gemm(x, lin["trellis"], lin["suh"], lin["svh"], 4, 0) for _ in range(3)]
+    for y in ys[1:]:
+        assert torch.equal(y, ys[0])
 
 
 def test_gemm_config3_sampled_rows(native, oracle):
