@@ -10,24 +10,21 @@
 // column group, then tile row, and the whole launch's units are cut into G nearly equal
 // contiguous ranges, one per workgroup (G = a few workgroups per CU, all resident at
 // once: there is no tail wave of workgroups).  A workgroup's range touches a few
-// *segments* (shard, column group); its waves take the range's units round-robin, so
-// the eight units a workgroup works on at once are the eight tile rows of one 128-input
-// block (segments start on block boundaries).
+// *segments* (shard, column group); its eight waves take eight contiguous runs of it.
 //
-// Per workgroup:
-//   1. each wave issues the loads of its first D units (D = 2..6 by K), so HBM is busy
-//      from the start; only the trellis words are loaded per unit;
-//   2. the activations fp16(H128(x * suh)) of every block the range touches are built once
-//      (one block per wave: FWHT across the wave) into an LDS table holding, per unit, its
-//      tile row's 16 values as duplicated fp16 pairs;
-//   3. main loop over the wave's units: a unit's K words per lane stream through the
-//      D-deep register ring; the tail-biting word before a lane's chunk is the previous
-//      lane's last word (DPP rotate within the tile's 8 lanes).  Each position is decoded
-//      with an SDWA add (or a 16-bit field for MCG), a v_mul_lo_u32 and a v_bitop3; the
-//      masked word meets its activation in a v_dot2c_f32_f16 whose second operand is
-//      broadcast by DPP from the lane that holds that activation row (both fp16 halves
-//      times x, summed in fp32);
-//   4. per segment, the waves' partial sums are added in a fixed order through LDS.  If the
+// Per wave:
+//   1. issue the loads of its first D units (D = 2..6 by K): the lane's K trellis words and
+//      its x and suh dwords of the unit's 128-input block, so HBM is busy from the start;
+//   2. main loop over the run: a unit's data streams through the D-deep register ring.
+//      Entering a new 128-input block (every 8 units), the wave transforms it,
+//      fp16(H128(x * suh)), and keeps the 128 results as one fp16 pair per lane; a unit of
+//      tile row t fetches lane 8t + l % 8's pair (one ds_bpermute) and duplicates each half.
+//      The tail-biting word before a lane's chunk is the previous lane's last word (DPP
+//      rotate within the tile's 8 lanes).  Each position is decoded with an SDWA add (or a
+//      16-bit field for MCG), a v_mul_lo_u32 and a v_bitop3; the masked word meets its
+//      activation in a v_dot2c_f32_f16 whose second operand is broadcast by DPP from the lane
+//      that holds that activation row (both fp16 halves times x, summed in fp32);
+//   3. per segment, the waves' partial sums are added in a fixed order through LDS.  If the
 //      segment lies inside this workgroup's range it is finished here; otherwise the
 //      partial goes to this workgroup's slot with agent-coherent stores, and the last of the
 //      segment's workgroups to arrive (a relaxed agent-scope counter in the workspace) has
@@ -52,7 +49,7 @@ constexpr int g1_depth(int K) { return (24 / (K + 3)) < 2 ? 2 : (24 / (K + 3)) >
 
 struct G1Shard {
     const uint32_t* trellis;   // (ic/16, oc/16, 8K) u32
-    const uint32_t* act;       // (ic/16, 16) activation pairs of this shard (gemv1_act_kernel)
+    const uint16_t* suh;       // (ic)
     const uint16_t* svh;       // (oc)
     uint16_t* C;               // (oc) fp16 output
     int ubeg;                  // first unit of the shard
@@ -163,32 +160,6 @@ __device__ __forceinline__ uint32_t g1_dup(float v)
     return h | (h << 16);
 }
 
-// ---------------------------------------------------------------- activation pass
-
-struct G1ActArgs {
-    const uint16_t* x;                 // (ic) fp16
-    int nsh, nblk;                     // shards, 128-input blocks per shard
-    const uint16_t* suh[G1_MAXSH];     // (ic) per shard
-    uint32_t* act[G1_MAXSH];           // (ic/16, 16) per shard
-};
-
-// fp16(H128(x * suh)) of every 128-input block, one wave per (shard, block), written as the
-// decode kernel reads it: tile row t of the block (16 inputs) is 16 dwords, dword r = fp16
-// value of row r duplicated in both halves.  Lane l ends the FWHT with outputs 2l, 2l + 1,
-// rows 2(l % 8), 2(l % 8) + 1 of tile row l / 8: one 8-byte store per lane.
-__global__ __launch_bounds__(256) void gemv1_act_kernel(const G1ActArgs a)
-{
-    const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (w >= a.nsh * a.nblk) return;   // whole waves only
-    const int s = w / a.nblk, b = w - s * a.nblk;
-    const uint32_t xw = reinterpret_cast<const uint32_t*>(a.x + b * 128)[lane];
-    const uint32_t sw = reinterpret_cast<const uint32_t*>(a.suh[s] + b * 128)[lane];
-    float v0 = g1_lo(xw) * g1_lo(sw), v1 = g1_hi(xw) * g1_hi(sw);
-    wave_fwht128(v0, v1);
-    *reinterpret_cast<uint2*>(a.act[s] + (8 * b + (lane >> 3)) * 16 + 2 * (lane & 7)) = uint2{g1_dup(v0), g1_dup(v1)};
-}
-
 // ---------------------------------------------------------------- decode kernel
 
 // Eight waves per SIMD need at most 64 VGPRs (measured on MI355X: 68 VGPRs leave room for
@@ -207,26 +178,23 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
 
-    // ---- this wave's units: ub + wave + G1_NW * j, j < n
-    const int n = (L > wave) ? (L - wave + G1_NW - 1) / G1_NW : 0;
+    // ---- this wave's units: the contiguous run ub + lo .. ub + lo + n - 1 of the range
+    const int lo = (wave * L) >> 3;
+    const int n = (((wave + 1) * L) >> 3) - lo;
     const uint32_t lk = lane * K;
-    const uint32_t la = 2 * (lane & 7);       // the lane's two activation rows in a tile row
     const bool first_lane = (lane & 7) == 0;
 
-    // Wave-uniform cursor over the wave's units: shard, column group, tile row, segment, the
-    // first word of the unit's 8 tiles and the unit's activation row.  Consecutive units of
-    // a wave are G1_NW tile rows apart (ntr >= 8, so a step crosses at most one
-    // column-group boundary); only such a crossing reads the shard table again.
+    // Wave-uniform cursor over the wave's units: shard, column group, tile row, segment and
+    // the first word of the unit's 8 tiles.  Consecutive units are consecutive tile rows
+    // (ntr >= 8); only a column-group crossing reads the shard table again.
     struct Cursor {
         int s, cg, tr, S;
-        long stride;   // words between tile rows G1_NW apart
+        long stride;   // words between consecutive tile rows
         const uint32_t* p;
-        const uint32_t* ap;
     };
     auto seat = [&](Cursor& q) {
-        q.stride = (long)G1_NW * sh(q.s).oc16 * (8 * K);
+        q.stride = (long)sh(q.s).oc16 * (8 * K);
         q.p = sh(q.s).trellis + ((long)q.tr * sh(q.s).oc16 + 8 * q.cg) * (8 * K);
-        q.ap = sh(q.s).act + q.tr * 16;
     };
     auto cursor_at = [&](int u) {
         Cursor q;
@@ -239,11 +207,10 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
         return q;
     };
     auto advance = [&](Cursor& q) {
-        q.tr += G1_NW;
+        q.tr++;
         q.p += q.stride;
-        q.ap += G1_NW * 16;
-        if (q.tr >= ntr) {
-            q.tr -= ntr;
+        if (q.tr == ntr) {
+            q.tr = 0;
             q.S++;
             if (++q.cg == sh(q.s).ncg) {
                 q.s++;
@@ -253,18 +220,21 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
         }
     };
 
-    // A unit's loads: the lane's K words and its activation pair.  Prefetch cursor (D units
+    // A unit's loads: the lane's K words, and the lane's x and suh dword of the unit's
+    // 128-input block (used when the unit starts a new block).  Prefetch cursor (D units
     // ahead; it stops at the wave's last unit, whose data is then loaded again and not used)
     // and processing cursor.
     struct Slot {
         uint32_t w[K + 1];
-        uint2 av;
+        uint32_t xw, sw;
     };
     auto load = [&](Slot& sl, const Cursor& q) {
         g1_load<K>(sl.w, q.p, lk);
-        sl.av = *reinterpret_cast<const uint2*>(q.ap + la);
+        const int blk = q.tr >> 3;
+        sl.xw = reinterpret_cast<const uint32_t*>(a.x + blk * 128)[lane];
+        sl.sw = reinterpret_cast<const uint32_t*>(sh(q.s).suh + blk * 128)[lane];
     };
-    Cursor pf = cursor_at(ub + wave), cu = pf;
+    Cursor pf = cursor_at(ub + lo), cu = pf;
     int jpf = 0;
     auto next_pf = [&]() -> const Cursor& {
         if (jpf + 1 < n) {
@@ -299,6 +269,12 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     // finished segment's sums to the wave's LDS row) sits between units, so each unit's work
     // is one basic block the scheduler can interleave; the loads sit outside every branch,
     // so the wait before a unit covers only that unit's own loads.
+    //
+    // Activations: when a unit enters a new 128-input block (every 8 units, or at a shard or
+    // column-group change) the wave transforms the block, fp16(H128(x * suh)) across the wave
+    // (lane l: outputs 2l, 2l + 1 = rows 2(l % 8), 2(l % 8) + 1 of tile row l / 8, kept as an
+    // fp16 pair); a unit of tile row t then reads lane 8t + l % 8's pair and duplicates each
+    // half for the v_dot2c broadcasts.
     const int o0 = (lane >> 3) * 16 + (lane & 7);
     float y0 = 0.f, y1 = 0.f;
     int cur = cu.S - S_first;
@@ -308,14 +284,27 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
         y0 = y1 = 0.f;
         cur = k;
     };
+    uint32_t bact = 0;
+    int bkey = -1;                            // (shard, block) of bact
     for (int j = 0; j < n; j += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
             if (d == 0 || j + d < n) {
                 if (cu.S - S_first != cur) flush(cu.S - S_first);
+                const int key = (cu.s << 24) | (cu.tr >> 3);
+                if (key != bkey) {
+                    bkey = key;
+                    float v0 = g1_lo(ring[d].xw) * g1_lo(ring[d].sw), v1 = g1_hi(ring[d].xw) * g1_hi(ring[d].sw);
+                    wave_fwht128(v0, v1);
+                    bact = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) |
+                           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
+                }
+                const uint32_t pr = (uint32_t)__builtin_amdgcn_ds_bpermute(((cu.tr & 7) * 8 + (lane & 7)) * 4, (int)bact);
+                const uint32_t a0 = __builtin_amdgcn_perm(pr, pr, 0x01000100u);
+                const uint32_t a1 = __builtin_amdgcn_perm(pr, pr, 0x03020302u);
                 chunk_prev_dpp<K>(ring[d].w, first_lane);
                 float acc[4] = {0.f, 0.f, 0.f, 0.f};
-                dot2_chunk<K, CB>(ring[d].w, ring[d].av.x, ring[d].av.y, acc, kc);
+                dot2_chunk<K, CB>(ring[d].w, a0, a1, acc, kc);
                 y0 += acc[0] + acc[1];
                 y1 += acc[2] + acc[3];
                 if (j + d + 1 < n) advance(cu);
@@ -474,11 +463,11 @@ static size_t g1_lds_bytes(int U, int G, int ntr)
 }
 
 // Per-shard share of the workspace after the counter area: slot rows for up to G1_GMAX
-// workgroups and one per column group, the shard's activation pairs (4 bytes per input) and
-// alignment slack.
+// workgroups and one per column group.
 size_t gemv1_slot_bytes(int ic, int oc)
 {
-    return (size_t)(G1_GMAX + oc / 128) * 128 * sizeof(float) + (size_t)ic * 4 + 256;
+    (void)ic;
+    return (size_t)(G1_GMAX + oc / 128) * 128 * sizeof(float);
 }
 
 int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint32_t* counters, int max_counters,
@@ -487,31 +476,9 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint
     const int ic = shards[0].ic;
     const int ntr = ic / 16;
 
-    // Workspace after the counter area: the activation pairs of every shard (ic 4-byte
-    // entries each), then per launch its slot rows.  One activation pass serves all shards.
-    const size_t act_bytes = ((size_t)nshards * ic * 4 + 255) & ~(size_t)255;
-    if (act_bytes > slot_bytes)
-        return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: slot area of %zu bytes, %zu needed", slot_bytes, act_bytes);
-    auto act_of = [&](int s) { return reinterpret_cast<uint32_t*>(slots + (size_t)s * ic * 4); };
-    for (int s0 = 0; s0 < nshards; s0 += G1_MAXSH) {
-        G1ActArgs aa = {};
-        aa.x = A;
-        aa.nsh = std::min(G1_MAXSH, nshards - s0);
-        aa.nblk = ic / 128;
-        for (int k = 0; k < aa.nsh; k++) {
-            aa.suh[k] = shards[s0 + k].suh;
-            aa.act[k] = act_of(s0 + k);
-        }
-        void* akargs[] = {&aa};
-        hipLaunchKernel(reinterpret_cast<const void*>(&gemv1_act_kernel), dim3((aa.nsh * aa.nblk + 3) / 4),
-                        dim3(256), akargs, 0, stream);
-        const int rc = check_launch("exl3_gemv (batch 1 activations)");
-        if (rc != EXL3_OK) return rc;
-    }
-
     bool done[EXL3_MAX_SHARDS] = {false};
     int cbase = 0;
-    size_t sbase = act_bytes;
+    size_t sbase = 0;
     const int gmax = std::min(G1_GMAX, G1_WG_PER_CU * g1_cu_count());
     for (int i = 0; i < nshards; i++) {
         if (done[i]) continue;
@@ -525,7 +492,7 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint
             const GemvShard& d = shards[s];
             G1Shard& e = args.sh[args.nshards++];
             e.trellis = d.trellis;
-            e.act = act_of(s);
+            e.suh = d.suh;
             e.svh = d.svh;
             e.C = d.C;
             e.ubeg = (int)U;
