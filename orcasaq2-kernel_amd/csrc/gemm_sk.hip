@@ -1,59 +1,108 @@
-// Prefill EXL3 GEMM for many activation rows, stream-K over 256 x 256 output tiles:
-//   C = fp16( H( Ah . W_q ) * svh ),  Ah = fp16(H(A * suh)) (had_r_128 pass, gemm.hip)
+// EXL3 GEMM, stream-K over BM x 256 output tiles (BM = 256 for prefill, 16 for 2..16-row
+// decode batches):
+//   C = fp16( H( Ah . W_q ) * svh ),  Ah = fp16(H(A * suh)) (a had_r_128 pass)
 // W_q is decoded from the packed trellis straight into LDS (never written to HBM), once per
-// 256-row tile, and multiplied with v_mfma_f32_16x16x32_f16.  Replaces the reconstruct
-// branch of orcasaq2/ops.py:50-59 (reconstruct -> hgemm_recon -> had_r_128) for row counts
-// where the decode cost spread over 256 rows is small next to the MFMA work.
+// BM-row tile, and multiplied with v_mfma_f32_16x16x32_f16.  Replaces the reconstruct
+// branch of orcasaq2/ops.py:50-59 (reconstruct -> hgemm_recon -> had_r_128) for many rows,
+// and the fused exl3_gemm of orcasaq2/ops.py:46-49 for 2..16 rows.
 //
-// Work decomposition.  Output tiles are 256 rows x 256 outputs (two output Hadamard blocks);
-// a tile is nks = ic / 64 K-steps of 64 inputs.  The tiles' K-steps, numbered tile-major,
-// are cut into G nearly equal contiguous ranges, one per workgroup, G = one per CU (all
-// resident): every CU does the same number of K-steps whatever the tile count ("stream-K").
-// A range covers at most a few tile pieces.  A piece that is a whole tile is finished by
-// its workgroup; a partial piece leaves its fp32 accumulators in a slot of the workspace,
-// and the last of the tile's workgroups to arrive (an agent-scope counter per tile) adds
-// the slots in workgroup order -- deterministic -- and finishes the tile.
+// Work decomposition.  Output tiles are BM rows x 256 outputs (two output Hadamard blocks);
+// a tile is nks = ic / 64 K-steps of 64 inputs.  The tiles' K-steps (all shards of a launch,
+// shard-major, then tile, then K-step) are cut into G nearly equal contiguous ranges, one
+// per workgroup ("stream-K"): every workgroup does the same number of K-steps whatever the
+// tile count.  A range covers a few tile pieces.  A piece that is a whole tile is finished
+// by its workgroup; a partial piece leaves its fp32 accumulators in a slot of the
+// workspace, and the last of the tile's workgroups to arrive (an agent-scope counter per
+// tile) adds the slots in workgroup order -- deterministic -- and finishes the tile.
 //
-// Per workgroup (8 waves, two per SIMD; wave w owns rows 128 (w / 4) .., outputs
-// 64 (w % 4) .. of the tile: 8 x 4 MFMA blocks, 128 fp32 accumulators per lane) and K-step:
-//   * the A tile (256 x 64 fp16) is loaded into registers one K-step ahead, then stored to
+// Per workgroup (8 waves; BM = 256: wave w owns rows 128 (w / 4) .., outputs 64 (w % 4) ..,
+// 8 x 4 MFMA blocks; BM = 16: wave w owns outputs 32 w .., 1 x 2 blocks) and K-step:
+//   * the A tile (BM x 64 fp16) is loaded into registers one K-step ahead, then stored to
 //     LDS rows of 72 halves (16-byte reads of 16 consecutive rows hit distinct banks);
 //   * the B tile is 4 tile rows x 16 tile columns = 512 chunks of 32 positions, one per
 //     lane: its K words are loaded one K-step ahead, the tail-biting word comes by DPP from
 //     the neighbouring lane, each masked word's fp16 halves are summed (the reconstruct
 //     rounding) and the chunk's two output columns' 16 inputs go to LDS as [output][input];
-//   * 2 x 12 LDS reads of 16 bytes feed 64 MFMAs.
-// Epilogue per 128-output block (two waves): rows through LDS, FWHT across a wave, * svh,
-// fp16 store.
+//   * LDS reads of 16 bytes feed the MFMAs.
+// Epilogue per 128-output block: rows through LDS, FWHT across a wave, * svh, fp16 store.
 #include "exl3_common.h"
 #include "exl3_launch.h"
 
 namespace exl3 {
 
 constexpr int SK_WAVES = 8;
-constexpr int SK_BM = 256;
 constexpr int SK_BN = 256;
 constexpr int SK_KS = 64;                     // inputs per K-step (4 tile rows)
 constexpr int SK_LD = SK_KS + 8;              // halves per LDS row of the A and B tiles
-constexpr int SK_ACC = 128;                   // fp32 accumulators per lane
-constexpr int SK_LDS = 2 * SK_BM * SK_LD * 2; // A + B tiles, bytes (73728)
-constexpr int SK_CLD = 128 + 4;               // floats per epilogue row in LDS
+constexpr int SK_CLD = 128 + 4;               // floats per epilogue row in LDS (BM = 256)
+constexpr int SK_MAXSH = 8;                   // shards per launch
+
+// Wave grid of a BM x 256 tile: WM x WN waves, each MB x NB blocks of 16 x 16.
+template <int BM>
+struct SkCfg;
+template <>
+struct SkCfg<256> { static constexpr int WM = 2, WN = 4, MB = 8, NB = 4; };
+template <>
+struct SkCfg<16> { static constexpr int WM = 1, WN = 8, MB = 1, NB = 2; };
+
+template <int BM>
+constexpr int sk_acc() { return SkCfg<BM>::MB * SkCfg<BM>::NB * 4; }   // fp32 accumulators per lane
+template <int BM>
+constexpr int sk_lds() { return (BM + SK_BN) * SK_LD * 2; }             // A + B tiles, bytes
+
+struct SkShard {
+    const uint16_t* Ah;        // (rows, ic) fp16, fp16(H(A * suh)) of this shard
+    const uint32_t* trellis;   // (ic/16, oc/16, 8K) u32
+    const uint16_t* svh;       // (oc)
+    uint16_t* C;               // (rows, ldc) fp16, columns [0, oc)
+    long ldc;
+    int oc, ntn, tbeg;         // outputs, 256-wide tile columns, first tile of the shard
+};
 
 struct SkArgs {
-    const uint16_t* Ah;        // (rows, ic) fp16, Hadamard-transformed activations
-    const uint32_t* trellis;   // (ic/16, oc/16, 8K) u32
-    uint16_t* C;               // (rows, oc) fp16
-    const uint16_t* svh;       // (oc)
     uint32_t* counters;        // one per tile, zeroed by sk_clear_kernel before the launch
-    float* slots;              // (tiles + G) x SK_WAVES x SK_ACC x 64 fp32
-    int rows, ic, oc, ntn, nks, ntiles;
+    float* slots;              // (tiles + G) x SK_WAVES x acc x 64 fp32
+    int rows, ic, nks, ntiles, nshards;
     int q, r;                  // K-steps per workgroup: q + (g < r)
+    SkShard sh[SK_MAXSH];
 };
 
 __global__ void sk_clear_kernel(uint32_t* counters, int n)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) counters[i] = 0u;
+}
+
+// Set-up of a 2..16-row launch in one kernel: the tile counters to zero and, for every
+// shard, its activations Ah = fp16(H128(A * suh)) (rows x ic), one wave per (shard, row,
+// 128-input block).
+struct SkPrepArgs {
+    const uint16_t* A;
+    int rows, ic, nsh, nblk;
+    const uint16_t* suh[SK_MAXSH];
+    uint16_t* Ah[SK_MAXSH];
+    uint32_t* counters;
+    int ntiles;
+};
+
+__global__ __launch_bounds__(256) void sk_prep_kernel(const SkPrepArgs a)
+{
+    const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (w < a.ntiles && lane == 0) a.counters[w] = 0u;
+    if (w >= a.nsh * a.rows * a.nblk) return;   // whole waves only
+    const int b = w % a.nblk, rs = w / a.nblk;
+    const int r = rs % a.rows, s = rs / a.rows;
+    const long off = (long)r * a.ic + b * 128;
+    const uint32_t xw = reinterpret_cast<const uint32_t*>(a.A + off)[lane];
+    const uint32_t sw = reinterpret_cast<const uint32_t*>(a.suh[s] + b * 128)[lane];
+    float v0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(xw & 0xffffu)) *
+               (float)__builtin_bit_cast(_Float16, (uint16_t)(sw & 0xffffu));
+    float v1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(xw >> 16)) *
+               (float)__builtin_bit_cast(_Float16, (uint16_t)(sw >> 16));
+    wave_fwht128(v0, v1);
+    reinterpret_cast<uint32_t*>(a.Ah[s] + off)[lane] =
+        (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
 }
 
 // First K-step (global numbering) of workgroup g, and the workgroup holding K-step u.
@@ -131,23 +180,27 @@ __device__ __forceinline__ void sk_load(uint32_t (&w)[K + 1], const uint32_t* __
     }
 }
 
-template <int K, int CB>
-__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_sk_kernel(const SkArgs a)
+template <int K, int CB, int BM>
+__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(BM == 256 ? 2 : 6, BM == 256 ? 2 : 6)))
+void gemm_sk_kernel(const SkArgs a)
 {
+    using Cfg = SkCfg<BM>;
+    constexpr int MB = Cfg::MB, NB = Cfg::NB, ACC = sk_acc<BM>();
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     _Float16* As = reinterpret_cast<_Float16*>(lds);
-    _Float16* Bs = As + SK_BM * SK_LD;
+    _Float16* Bs = As + BM * SK_LD;
 
     const int g = blockIdx.x;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
-    const int wm = wave >> 2, wn = wave & 3;
-    const int tc = a.oc >> 4;                 // tile columns of W_q
+    const int wm = wave / Cfg::WN, wn = wave % Cfg::WN;
     const Dot2Consts kc = dot2_consts();
 
-    // A-tile loader: thread t moves 16 bytes of rows 64 p + t / 8, p = 0..3, segment t % 8.
+    // A-tile loader: thread t moves 16 bytes of row t / 8 (+ 64 p), segment t % 8.
     const int arow = tid >> 3, aseg = tid & 7;
+    constexpr int AP = BM >= 64 ? BM / 64 : 1;       // passes
+    const bool aload = BM >= 64 || arow < BM;
     // B chunk of this thread: chunk id tid = 8 * tile + c, tile = 16 ti_l + tn_l (a tile's
     // 8 chunks on 8 consecutive lanes)
     const int c = lane & 7;
@@ -155,8 +208,8 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(2
     const int btile = tid >> 3;
     const int bn0 = 16 * (btile & 15) + c, bk0 = 16 * (btile >> 4);
 
-    f32x4 acc[8][4];
-    uint4 areg[4];
+    f32x4 acc[MB][NB];
+    uint4 areg[AP];
     uint32_t w[K + 1];
 
     const long u_begin = sk_first(a, g), u_end = sk_first(a, g + 1);
@@ -165,26 +218,33 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(2
         const int t = (int)(u / a.nks);
         const int s0 = (int)(u - (long)t * a.nks);
         const int s1 = (int)min((long)a.nks, s0 + (u_end - u));
-        const int tm = t / a.ntn, tn = t - tm * a.ntn;
-        const int m0 = tm * SK_BM;
+        int si = 0;
+#pragma unroll
+        for (int i = 1; i < SK_MAXSH; i++)
+            if (i < a.nshards && t >= a.sh[i].tbeg) si = i;
+        const SkShard& S = a.sh[si];
+        const int tl = t - S.tbeg;
+        const int tm = tl / S.ntn, tn = tl - tm * S.ntn;
+        const int m0 = tm * BM;
+        const int tc = S.oc >> 4;                    // tile columns of W_q
         const int btn = 16 * tn + (btile & 15);
         const bool bok = btn < tc;
 
         auto load_step = [&](int s) {
 #pragma unroll
-            for (int p = 0; p < 4; p++) {
+            for (int p = 0; p < AP; p++) {
                 const int row = m0 + 64 * p + arow;
-                areg[p] = row < a.rows
-                    ? *reinterpret_cast<const uint4*>(a.Ah + (long)row * a.ic + s * SK_KS + aseg * 8)
+                areg[p] = (aload && row < a.rows)
+                    ? *reinterpret_cast<const uint4*>(S.Ah + (long)row * a.ic + s * SK_KS + aseg * 8)
                     : uint4{0u, 0u, 0u, 0u};
             }
             const int ti = 4 * s + (btile >> 4);
-            sk_load<K>(w, a.trellis + ((long)ti * tc + (bok ? btn : 0)) * (8 * K) + c * K, bok);
+            sk_load<K>(w, S.trellis + ((long)ti * tc + (bok ? btn : 0)) * (8 * K) + c * K, bok);
         };
         auto store_step = [&]() {
 #pragma unroll
-            for (int p = 0; p < 4; p++)
-                *reinterpret_cast<uint4*>(As + (64 * p + arow) * SK_LD + aseg * 8) = areg[p];
+            for (int p = 0; p < AP; p++)
+                if (aload) *reinterpret_cast<uint4*>(As + (64 * p + arow) * SK_LD + aseg * 8) = areg[p];
             chunk_prev_dpp<K>(w, first_lane);
             uint4 o[4];
             sk_decode<K, CB>(w, kc, o);
@@ -195,9 +255,9 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(2
         };
 
 #pragma unroll
-        for (int mb = 0; mb < 8; mb++)
+        for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-            for (int nb = 0; nb < 4; nb++) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
         load_step(s0);
         for (int s = s0; s < s1; s++) {
@@ -207,17 +267,17 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(2
             if (s + 1 < s1) load_step(s + 1);
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                f16x8 bf[4];
+                f16x8 bf[NB];
 #pragma unroll
-                for (int nb = 0; nb < 4; nb++)
-                    bf[nb] = *reinterpret_cast<const f16x8*>(Bs + (64 * wn + 16 * nb + (lane & 15)) * SK_LD + 32 * h +
-                                                             8 * (lane >> 4));
+                for (int nb = 0; nb < NB; nb++)
+                    bf[nb] = *reinterpret_cast<const f16x8*>(Bs + (NB * 16 * wn + 16 * nb + (lane & 15)) * SK_LD +
+                                                             32 * h + 8 * (lane >> 4));
 #pragma unroll
-                for (int mb = 0; mb < 8; mb++) {
-                    const f16x8 af = *reinterpret_cast<const f16x8*>(As + (128 * wm + 16 * mb + (lane & 15)) * SK_LD +
+                for (int mb = 0; mb < MB; mb++) {
+                    const f16x8 af = *reinterpret_cast<const f16x8*>(As + (MB * 16 * wm + 16 * mb + (lane & 15)) * SK_LD +
                                                                      32 * h + 8 * (lane >> 4));
 #pragma unroll
-                    for (int nb = 0; nb < 4; nb++) acc[mb][nb] = mfma16x16x32(af, bf[nb], acc[mb][nb]);
+                    for (int nb = 0; nb < NB; nb++) acc[mb][nb] = mfma16x16x32(af, bf[nb], acc[mb][nb]);
                 }
             }
         }
@@ -227,15 +287,15 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(2
         bool finish = s0 == 0 && s1 == a.nks;
         if (!finish) {
             const int g_lo = sk_wg_of(a, (long)t * a.nks), g_hi = sk_wg_of(a, (long)(t + 1) * a.nks - 1);
-            uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + ((long)(t + g) * SK_WAVES + wave) * SK_ACC * 64) + lane;
+            uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + ((long)(t + g) * SK_WAVES + wave) * ACC * 64) + lane;
 #pragma unroll
-            for (int mb = 0; mb < 8; mb++)
+            for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-                for (int nb = 0; nb < 4; nb++) {
+                for (int nb = 0; nb < NB; nb++) {
                     const f32x4 v = acc[mb][nb];
-                    __hip_atomic_store(my + (long)((mb * 4 + nb) * 2) * 64, sk_pack2(v.x, v.y), __ATOMIC_RELAXED,
+                    __hip_atomic_store(my + (long)((mb * NB + nb) * 2) * 64, sk_pack2(v.x, v.y), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(my + (long)((mb * 4 + nb) * 2 + 1) * 64, sk_pack2(v.z, v.w), __ATOMIC_RELAXED,
+                    __hip_atomic_store(my + (long)((mb * NB + nb) * 2 + 1) * 64, sk_pack2(v.z, v.w), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
                 }
             __builtin_amdgcn_s_waitcnt(0);   // this wave's slot stores are complete
@@ -251,19 +311,19 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(2
             if (finish) {
                 // last to arrive: every contributor's stores completed before its increment
 #pragma unroll
-                for (int mb = 0; mb < 8; mb++)
+                for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-                    for (int nb = 0; nb < 4; nb++) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
                 for (int gg = g_lo; gg <= g_hi; gg++) {
                     const uint64_t* sl =
-                        reinterpret_cast<const uint64_t*>(a.slots + ((long)(t + gg) * SK_WAVES + wave) * SK_ACC * 64) + lane;
+                        reinterpret_cast<const uint64_t*>(a.slots + ((long)(t + gg) * SK_WAVES + wave) * ACC * 64) + lane;
 #pragma unroll
-                    for (int mb = 0; mb < 8; mb++)
+                    for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-                        for (int nb = 0; nb < 4; nb++) {
-                            const uint64_t p = __hip_atomic_load(sl + (long)((mb * 4 + nb) * 2) * 64, __ATOMIC_RELAXED,
+                        for (int nb = 0; nb < NB; nb++) {
+                            const uint64_t p = __hip_atomic_load(sl + (long)((mb * NB + nb) * 2) * 64, __ATOMIC_RELAXED,
                                                                  __HIP_MEMORY_SCOPE_AGENT);
-                            const uint64_t q = __hip_atomic_load(sl + (long)((mb * 4 + nb) * 2 + 1) * 64,
+                            const uint64_t q = __hip_atomic_load(sl + (long)((mb * NB + nb) * 2 + 1) * 64,
                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                             acc[mb][nb] += f32x4{__builtin_bit_cast(float, (uint32_t)p),
                                                  __builtin_bit_cast(float, (uint32_t)(p >> 32)),
@@ -274,36 +334,53 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(2
             }
         }
         if (finish) {
-            // Output block ob (128 outputs) of rows 128 wm ..: waves wn = 2 ob' and 2 ob' + 1 hold
-            // its two 64-column halves.  16 rows at a time through LDS (16 x 132 floats per block
-            // and row half), then wave (wn & 1) transforms rows 8 (wn & 1) .. + 7: FWHT, * svh,
-            // fp16 store.
-            const int blk = wn >> 1, half = wn & 1;
-            float* cs = reinterpret_cast<float*>(lds) + (wm * 2 + blk) * 16 * SK_CLD;
-            const int ob = 16 * tn + 8 * blk;         // tile column of the block's first output
-            const bool col_ok = ob < tc;
-            const uint32_t sv = col_ok ? reinterpret_cast<const uint32_t*>(a.svh + ob * 16)[lane] : 0u;
-            const float sv0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv & 0xffffu));
-            const float sv1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv >> 16));
+            auto store_row = [&](int row, int ob, float v0, float v1) {
+                // ob: tile column of the 128-output block's first output
+                wave_fwht128(v0, v1);
+                if (ob < tc && row < a.rows) {
+                    const uint32_t sv = reinterpret_cast<const uint32_t*>(S.svh + ob * 16)[lane];
+                    const float sv0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv & 0xffffu));
+                    const float sv1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv >> 16));
+                    const uint32_t o = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v0 * sv0)) |
+                                       ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v1 * sv1)) << 16);
+                    reinterpret_cast<uint32_t*>(S.C + (long)row * S.ldc + ob * 16)[lane] = o;
+                }
+            };
             __syncthreads();                  // every wave is done with the A/B tiles
-            for (int mb = 0; mb < 8; mb++) {
+            if constexpr (BM == 256) {
+                // Output block of rows 128 wm ..: waves wn = 2 blk and 2 blk + 1 hold its two
+                // 64-column halves.  16 rows at a time through LDS (16 x 132 floats per block
+                // and row half), then wave (wn & 1) transforms rows 8 (wn & 1) .. + 7.
+                const int blk = wn >> 1, half = wn & 1;
+                float* cs = reinterpret_cast<float*>(lds) + (wm * 2 + blk) * 16 * SK_CLD;
+                for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
-                for (int nb = 0; nb < 4; nb++)
+                    for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            cs[(4 * (lane >> 4) + e) * SK_CLD + 64 * half + 16 * nb + (lane & 15)] = acc[mb][nb][e];
+                    __syncthreads();
+                    for (int r = 8 * half; r < 8 * half + 8; r++)
+                        store_row(m0 + 128 * wm + 16 * mb + r, 16 * tn + 8 * blk, cs[r * SK_CLD + 2 * lane],
+                                  cs[r * SK_CLD + 2 * lane + 1]);
+                    __syncthreads();
+                }
+            } else {
+                // the whole 16 x 256 tile in LDS (16 rows of 260 floats); wave w transforms
+                // (row, block) pairs w, w + 8, w + 16, w + 24
+                constexpr int LD = SK_BN + 4;
+                float* cs = reinterpret_cast<float*>(lds);
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
 #pragma unroll
                     for (int e = 0; e < 4; e++)
-                        cs[(4 * (lane >> 4) + e) * SK_CLD + 64 * half + 16 * nb + (lane & 15)] = acc[mb][nb][e];
+                        cs[(4 * (lane >> 4) + e) * LD + NB * 16 * wn + 16 * nb + (lane & 15)] = acc[0][nb][e];
                 __syncthreads();
-                for (int r = 8 * half; r < 8 * half + 8; r++) {
-                    float v0 = cs[r * SK_CLD + 2 * lane], v1 = cs[r * SK_CLD + 2 * lane + 1];
-                    wave_fwht128(v0, v1);
-                    const int row = m0 + 128 * wm + 16 * mb + r;
-                    if (col_ok && row < a.rows) {
-                        const uint32_t o = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v0 * sv0)) |
-                                           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v1 * sv1)) << 16);
-                        reinterpret_cast<uint32_t*>(a.C + (long)row * a.oc + ob * 16)[lane] = o;
-                    }
+                for (int j = wave; j < 32; j += SK_WAVES) {
+                    const int r = j & 15, blk = j >> 4;
+                    store_row(m0 + r, 16 * tn + 8 * blk, cs[r * LD + 128 * blk + 2 * lane],
+                              cs[r * LD + 128 * blk + 2 * lane + 1]);
                 }
-                __syncthreads();
             }
         }
         __syncthreads();                      // LDS is free for the next piece
@@ -312,11 +389,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(2
 
 // ---------------------------------------------------------------- host side
 
-size_t gemm_sk_slot_bytes(int rows, int oc, int G)
-{
-    const long tiles = (long)((rows + SK_BM - 1) / SK_BM) * ((oc + SK_BN - 1) / SK_BN);
-    return ((size_t)tiles * 4 + 255) / 256 * 256 + (size_t)(tiles + G) * SK_WAVES * SK_ACC * 64 * sizeof(float);
-}
+static inline size_t sk_align(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int gemm_sk_cus()
 {
@@ -326,54 +399,157 @@ int gemm_sk_cus()
     return cus;
 }
 
-template <int K, int CB>
-static const void* sk_fn() { return reinterpret_cast<const void*>(&gemm_sk_kernel<K, CB>); }
+// Workgroups per launch: BM = 256 keeps one per CU (two waves per SIMD), BM = 16 three.
+template <int BM>
+static int sk_gmax() { return (BM == 256 ? 1 : 3) * gemm_sk_cus(); }
 
-int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
-                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, int G, hipStream_t stream)
+template <int BM>
+static size_t sk_slot() { return (size_t)SK_WAVES * sk_acc<BM>() * 64 * sizeof(float); }
+
+static int sk_ntn(int oc) { return (oc + SK_BN - 1) / SK_BN; }
+
+// Counters and slots of one launch of `tiles` tiles and up to G workgroups.
+template <int BM>
+static size_t sk_ws(long tiles, int G) { return sk_align((size_t)tiles * 4) + (size_t)(tiles + G) * sk_slot<BM>(); }
+
+size_t gemm_sk_slot_bytes(int rows, int oc, int G)
 {
-    SkArgs a = {};
-    a.Ah = Ah;
-    a.trellis = trellis;
-    a.C = C;
-    a.svh = svh;
-    a.rows = rows;
-    a.ic = ic;
-    a.oc = oc;
-    a.ntn = (oc + SK_BN - 1) / SK_BN;
-    a.nks = ic / SK_KS;
-    a.ntiles = ((rows + SK_BM - 1) / SK_BM) * a.ntn;
+    return sk_ws<256>((long)((rows + 255) / 256) * sk_ntn(oc), G);
+}
+
+// Per-shard workspace of the 2..16-row GEMV: its activations fp16(H(A * suh)), then its
+// share of counters and slots (each launch has at least one shard, so the shares cover it).
+size_t gemv_sk_bytes(int rows, int ic, int oc)
+{
+    return sk_align((size_t)rows * ic * 2) + sk_ws<16>(sk_ntn(oc), sk_gmax<16>());
+}
+
+template <int K, int CB, int BM>
+static const void* sk_fn() { return reinterpret_cast<const void*>(&gemm_sk_kernel<K, CB, BM>); }
+
+template <int BM>
+static const void* sk_fn_kcb(int K, int cb)
+{
+#define EXL3_CASE(KK) case KK: return cb == CB_MCG ? sk_fn<KK, CB_MCG, BM>() : sk_fn<KK, CB_3INST, BM>();
+    switch (K) {
+        EXL3_CASE(1) EXL3_CASE(2) EXL3_CASE(3) EXL3_CASE(4)
+        EXL3_CASE(5) EXL3_CASE(6) EXL3_CASE(7) EXL3_CASE(8)
+    }
+#undef EXL3_CASE
+    return nullptr;
+}
+
+// One stream-K launch over a.sh[0 .. nshards): clears its tile counters, then runs.  `ws`
+// holds the counters and slots (sk_ws bytes).
+template <int BM>
+static int sk_launch(SkArgs& a, int K, int cb, char* ws, size_t ws_bytes, const char* what, hipStream_t stream,
+                     bool clear = true)
+{
     const long units = (long)a.ntiles * a.nks;
-    // at least 16 K-steps per workgroup: a tile has at most nks / 16 + 2 contributors
-    if (G > units / 16) G = (int)std::max<long>(1, units / 16);
-    const size_t cbytes = ((size_t)a.ntiles * 4 + 255) / 256 * 256;
-    // fewer workgroups when the workspace was sized on a device with fewer CUs
-    const size_t slot = (size_t)SK_WAVES * SK_ACC * 64 * sizeof(float);
-    const long fit = ws_bytes > cbytes ? (long)((ws_bytes - cbytes) / slot) - a.ntiles : 0;
+    // at least 8 K-steps per workgroup: a tile has at most nks / 8 + 2 contributors
+    int G = (int)std::min<long>(sk_gmax<BM>(), std::max<long>(1, units / 8));
+    const size_t cbytes = sk_align((size_t)a.ntiles * 4);
+    const long fit = ws_bytes > cbytes ? (long)((ws_bytes - cbytes) / sk_slot<BM>()) - a.ntiles : 0;
     if (fit < 1)
-        return set_error(EXL3_ERR_WORKSPACE, "exl3_gemm: workspace of %zu bytes, %zu needed", ws_bytes,
-                         gemm_sk_slot_bytes(rows, oc, G));
-    if (G > fit) G = (int)fit;
+        return set_error(EXL3_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", what, ws_bytes,
+                         sk_ws<BM>(a.ntiles, G));
+    if (G > fit) G = (int)fit;   // a workspace sized on a device with fewer CUs
     a.q = (int)(units / G);
     a.r = (int)(units % G);
     a.counters = reinterpret_cast<uint32_t*>(ws);
     a.slots = reinterpret_cast<float*>(ws + cbytes);
-    hipLaunchKernelGGL(sk_clear_kernel, dim3((a.ntiles + 255) / 256), dim3(256), 0, stream, a.counters, a.ntiles);
-    int rc = check_launch("exl3_gemm (counters)");
-    if (rc != EXL3_OK) return rc;
-    const void* fn = nullptr;
-#define EXL3_CASE(KK) case KK: fn = cb == CB_MCG ? sk_fn<KK, CB_MCG>() : sk_fn<KK, CB_3INST>(); break;
-    switch (K) {
-        EXL3_CASE(1) EXL3_CASE(2) EXL3_CASE(3) EXL3_CASE(4)
-        EXL3_CASE(5) EXL3_CASE(6) EXL3_CASE(7) EXL3_CASE(8)
-        default: return set_error(EXL3_ERR_ARG, "exl3_gemm: K=%d is not in 1..8", K);
+    if (clear) {
+        hipLaunchKernelGGL(sk_clear_kernel, dim3((a.ntiles + 255) / 256), dim3(256), 0, stream, a.counters, a.ntiles);
+        const int rc = check_launch(what);
+        if (rc != EXL3_OK) return rc;
     }
-#undef EXL3_CASE
-    hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, SK_LDS);
-    (void)hipGetLastError();
+    const void* fn = sk_fn_kcb<BM>(K, cb);
+    if (!fn) return set_error(EXL3_ERR_ARG, "%s: K=%d is not in 1..8", what, K);
+    if (sk_lds<BM>() > 64 * 1024) {
+        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, sk_lds<BM>());
+        (void)hipGetLastError();
+    }
     void* kargs[] = {&a};
-    hipLaunchKernel(fn, dim3(G), dim3(64 * SK_WAVES), kargs, SK_LDS, stream);
-    return check_launch("exl3_gemm (stream-K)");
+    hipLaunchKernel(fn, dim3(G), dim3(64 * SK_WAVES), kargs, sk_lds<BM>(), stream);
+    return check_launch(what);
+}
+
+int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
+                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, int G, hipStream_t stream)
+{
+    (void)G;
+    SkArgs a = {};
+    a.rows = rows;
+    a.ic = ic;
+    a.nks = ic / SK_KS;
+    a.nshards = 1;
+    SkShard& s = a.sh[0];
+    s.Ah = Ah;
+    s.trellis = trellis;
+    s.svh = svh;
+    s.C = C;
+    s.ldc = oc;
+    s.oc = oc;
+    s.ntn = sk_ntn(oc);
+    s.tbeg = 0;
+    a.ntiles = ((rows + 255) / 256) * s.ntn;
+    return sk_launch<256>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
+}
+
+// 2..16 rows: per (K, codebook) group of up to SK_MAXSH shards, one set-up kernel (the
+// shards' activations, the group's tile counters) and one stream-K launch with 16-row tiles.
+int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws, size_t ws_bytes,
+                     hipStream_t stream)
+{
+    const int ic = shards[0].ic;
+    bool done[EXL3_MAX_SHARDS] = {false};
+    size_t off = 0;
+    const size_t ah = sk_align((size_t)rows * ic * 2);
+    for (int i = 0; i < nshards; i++) {
+        if (done[i]) continue;
+        SkArgs a = {};
+        SkPrepArgs p = {};
+        a.rows = p.rows = rows;
+        a.ic = p.ic = ic;
+        a.nks = ic / SK_KS;
+        p.A = A;
+        p.nblk = ic / 128;
+        int tiles = 0;
+        for (int s = i; s < nshards && a.nshards < SK_MAXSH; s++) {
+            if (done[s] || shards[s].K != shards[i].K || shards[s].cb != shards[i].cb) continue;
+            const GemvShard& d = shards[s];
+            if (off + ah > ws_bytes)
+                return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: workspace of %zu bytes is too small", ws_bytes);
+            uint16_t* Ah = reinterpret_cast<uint16_t*>(ws + off);
+            off += ah;
+            p.suh[a.nshards] = d.suh;
+            p.Ah[a.nshards] = Ah;
+            SkShard& e = a.sh[a.nshards++];
+            e.Ah = Ah;
+            e.trellis = d.trellis;
+            e.svh = d.svh;
+            e.C = d.C;
+            e.ldc = d.ldc;
+            e.oc = d.oc;
+            e.ntn = sk_ntn(d.oc);
+            e.tbeg = tiles;
+            tiles += e.ntn;
+            done[s] = true;
+        }
+        a.ntiles = p.ntiles = tiles;
+        p.nsh = a.nshards;
+        p.counters = reinterpret_cast<uint32_t*>(ws + off);
+        const int waves = std::max(p.nsh * rows * p.nblk, tiles);
+        hipLaunchKernelGGL(sk_prep_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
+        int rc = check_launch("exl3_gemv (set-up)");
+        if (rc != EXL3_OK) return rc;
+        const size_t need = sk_ws<16>(tiles, sk_gmax<16>());
+        const size_t avail = ws_bytes > off ? ws_bytes - off : 0;
+        rc = sk_launch<16>(a, shards[i].K, shards[i].cb, ws + off, std::min(need, avail), "exl3_gemv", stream, false);
+        if (rc != EXL3_OK) return rc;
+        off += std::min(need, avail);
+    }
+    return EXL3_OK;
 }
 
 }  // namespace exl3

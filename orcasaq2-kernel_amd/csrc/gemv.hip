@@ -2,7 +2,11 @@
 //   C = fp16( H( fp16(H(A * suh)) . W_q ) * svh )
 // with W_q decoded from the packed trellis on the fly and never written anywhere.
 // Replaces exllamav3_ext.exl3_gemm as called at orcasaq2/ops.py:46-49 (rows <= 144 there;
-// this path takes rows <= 16 and the MFMA GEMM takes the rest).
+// this path takes rows <= 16 and the MFMA GEMM takes the rest).  Row counts:
+//   * 1: gemv1.hip (persistent decode with v_dot2c);
+//   * 2..GV_SPLIT_MAX_ROWS: the two kernels below;
+//   * above: gemm_sk.hip with 16-row tiles (decode into LDS once per tile, MFMA from LDS;
+//     the cost hardly depends on the row count).
 //
 // Two kernels, no inter-workgroup synchronisation inside a kernel (an agent-scope fence
 // on this part writes back and invalidates the whole per-XCD L2, which serialises):
@@ -25,6 +29,7 @@ namespace exl3 {
 
 constexpr int GV_WAVES = 4;
 constexpr int GV_MAX_ROWS = 16;
+constexpr int GV_SPLIT_MAX_ROWS = 4;                   // more rows: gemm_sk.hip, 16-row tiles
 constexpr int GV_MAX_BLKS = 8;                          // 128-input blocks per workgroup (even)
 constexpr int GV_HX_ROW = GV_MAX_BLKS * 8 * 16 + 4;     // u32 per LDS activation row (16 B per tile row and m)
 constexpr int GV_GROUP = 8;                             // shards per launch
@@ -69,6 +74,7 @@ static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 size_t gemv_workspace_bytes(int rows, int ic, int oc)
 {
     if (rows == 1) return align256(gemv1_slot_bytes(ic, oc));
+    if (rows > GV_SPLIT_MAX_ROWS) return align256(gemv_sk_bytes(rows, ic, oc));
     return align256((size_t)gemv_splits(ic, oc) * rows * oc * sizeof(float));
 }
 
@@ -298,6 +304,9 @@ int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int r
         return gemv1_dispatch(A, shards, nshards, reinterpret_cast<uint32_t*>(ws),
                               (int)(GEMV_COUNTER_BYTES / sizeof(uint32_t)), ws + GEMV_COUNTER_BYTES,
                               offs[nshards] - GEMV_COUNTER_BYTES, stream);
+    if (rows > GV_SPLIT_MAX_ROWS)
+        return gemv_sk_dispatch(A, shards, nshards, rows, ws + GEMV_COUNTER_BYTES, offs[nshards] - GEMV_COUNTER_BYTES,
+                                stream);
     bool done[EXL3_MAX_SHARDS] = {false};
     const size_t lds = hx_bytes(rows);
     for (int i = 0; i < nshards; i++) {

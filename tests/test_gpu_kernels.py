@@ -114,8 +114,9 @@ def check_linear_out(y, x, lin, cb, oracle, W=None):
 
 
 @pytest.mark.parametrize("K", range(1, 9))
-@pytest.mark.parametrize("rows", [1, 4, 16])
+@pytest.mark.parametrize("rows", [1, 4, 5, 16])
 def test_gemv_small_all_K(native, oracle, K, rows):
+    """1 row: the persistent kernel; 2..4: the split kernels; 5..16: 16-row stream-K tiles"""
     lin = syn.linear(512, 384, K, seed=100 + K)
     x = syn.activations(rows, 512, torch.Generator().manual_seed(rows))
     d = to_gpu(lin)
