@@ -105,6 +105,16 @@ __global__ __launch_bounds__(256) void sk_prep_kernel(const SkPrepArgs a)
         (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
 }
 
+// Logical workgroup of launch slot b.  Launch slots go to the 8 XCDs round-robin (slot b on
+// XCD b % 8), so when G is a multiple of 8 each XCD gets a contiguous block of logical
+// workgroups -- for a 256-row GEMM, the tiles of one row block: their A rows are shared
+// in that XCD's L2.  Any placement gives the same results; this one only saves traffic.
+__device__ __forceinline__ int sk_logical(int b)
+{
+    const int G = gridDim.x;
+    return (G & 7) ? b : (b & 7) * (G >> 3) + (b >> 3);
+}
+
 // First K-step (global numbering) of workgroup g, and the workgroup holding K-step u.
 __device__ __forceinline__ long sk_first(const SkArgs& a, int g) { return (long)g * a.q + min(g, a.r); }
 __device__ __forceinline__ int sk_wg_of(const SkArgs& a, long u)
@@ -190,7 +200,7 @@ void gemm_sk_kernel(const SkArgs a)
     _Float16* As = reinterpret_cast<_Float16*>(lds);
     _Float16* Bs = As + BM * SK_LD;
 
-    const int g = blockIdx.x;
+    const int g = sk_logical(blockIdx.x);
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
