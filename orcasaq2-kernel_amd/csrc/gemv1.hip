@@ -73,24 +73,39 @@ __device__ __forceinline__ int g1_div(int x, G1Div d)
     return (int)(__umulhi((uint32_t)x, d.m) >> d.sh);
 }
 
-struct G1Args {
+// One group of shards with the same K and codebook, decoded by G workgroups.
+struct G1Group {
     const uint16_t* x;         // (ic) fp16
     uint32_t* counters;        // one per segment; zero between calls
     float* slots;              // (G + segments) x 128 fp32
     int U, G, ntr, nshards, nsegs;
     int q, r;                  // U = q G + r: workgroup g owns q + (g < r) units
     G1Div dntr, dq, dq1;       // division by ntr, q, q + 1
+};
+
+// A launch of one group (shards 0 .. nshards - 1 of the table).
+struct G1Args {
+    G1Group grp;
     G1Shard sh[G1_MAXSH];
 };
 
+// A launch of several groups of one codebook, one K each: group i owns workgroups
+// gbeg[i] .. gbeg[i + 1] - 1 and shards sh0[i] .. sh0[i] + grp[i].nshards - 1.
+struct G1Multi {
+    G1Group grp[G1_MAXSH];
+    G1Shard sh[G1_MAXSH];
+    int gbeg[G1_MAXSH], sh0[G1_MAXSH], K[G1_MAXSH];
+    int ngrp;
+};
+
 // First unit of workgroup g: the first r workgroups own q + 1 units, the others q.
-__device__ __forceinline__ int g1_first_unit(const G1Args& a, int g)
+__device__ __forceinline__ int g1_first_unit(const G1Group& a, int g)
 {
     return g * a.q + min(g, a.r);
 }
 
 // Workgroup whose unit range holds unit u.
-__device__ __forceinline__ int g1_wg_of(const G1Args& a, int u)
+__device__ __forceinline__ int g1_wg_of(const G1Group& a, int u)
 {
     const int big = a.r * (a.q + 1);
     return u < big ? g1_div(u, a.dq1) : a.r + g1_div(u - big, a.dq);
@@ -100,25 +115,25 @@ __device__ __forceinline__ int g1_wg_of(const G1Args& a, int u)
 // scalar loads of the whole table issue together instead of as a chain of dependent loads
 // (each a few hundred cycles); a single-shard launch (ONE) reads nothing.
 template <bool ONE>
-__device__ __forceinline__ int g1_shard_of_seg(const G1Args& a, int S)
+__device__ __forceinline__ int g1_shard_of_seg(const G1Group& a, const G1Shard* sht, int S)
 {
     int s = 0;
     if constexpr (!ONE) {
 #pragma unroll
         for (int i = 1; i < G1_MAXSH; i++)
-            if (i < a.nshards && S >= a.sh[i].sbeg) s = i;
+            if (i < a.nshards && S >= sht[i].sbeg) s = i;
     }
     return s;
 }
 
 template <bool ONE>
-__device__ __forceinline__ int g1_shard_of_unit(const G1Args& a, int u)
+__device__ __forceinline__ int g1_shard_of_unit(const G1Group& a, const G1Shard* sht, int u)
 {
     int s = 0;
     if constexpr (!ONE) {
 #pragma unroll
         for (int i = 1; i < G1_MAXSH; i++)
-            if (i < a.nshards && u >= a.sh[i].ubeg) s = i;
+            if (i < a.nshards && u >= sht[i].ubeg) s = i;
     }
     return s;
 }
@@ -162,17 +177,14 @@ __device__ __forceinline__ uint32_t g1_dup(float v)
 
 // ---------------------------------------------------------------- decode kernel
 
-// Eight waves per SIMD need at most 64 VGPRs (measured on MI355X: 68 VGPRs leave room for
-// only 6); the SGPR cap keeps the count well inside what eight waves per SIMD may hold.
+// Workgroup g of group a (shard table sht) -- the whole kernel body.
 template <int K, int CB, bool ONE>
-__global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8), amdgpu_num_sgpr(74))) void gemv1_kernel(const G1Args a)
+__device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, const int g, uint32_t* lds)
 {
-    // shard table entry; a single-shard launch (ONE) only ever reads entry 0 (constant offsets)
-    auto sh = [&](int s) -> const G1Shard& { return a.sh[ONE ? 0 : s]; };
-    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    // shard table entry; a single-shard group (ONE) only ever reads entry 0
+    auto sh = [&](int s) -> const G1Shard& { return sht[ONE ? 0 : s]; };
     constexpr int D = g1_depth(K);
 
-    const int g = blockIdx.x;
     const int ntr = a.ntr;
     const int ub = g1_first_unit(a, g), L = a.q + (g < a.r ? 1 : 0);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -198,7 +210,7 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     };
     auto cursor_at = [&](int u) {
         Cursor q;
-        q.s = g1_shard_of_unit<ONE>(a, u);
+        q.s = g1_shard_of_unit<ONE>(a, sht, u);
         const int rel = u - sh(q.s).ubeg;
         q.cg = g1_div(rel, a.dntr);
         q.tr = rel - q.cg * ntr;
@@ -220,20 +232,12 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
         }
     };
 
-    // A unit's loads: the lane's K words, and the lane's x and suh dword of the unit's
-    // 128-input block (used when the unit starts a new block).  Prefetch cursor (D units
-    // ahead; it stops at the wave's last unit, whose data is then loaded again and not used)
-    // and processing cursor.
+    // A unit's loads: the lane's K words.  Prefetch cursor (D units ahead; it stops at the
+    // wave's last unit, whose data is then loaded again and not used) and processing cursor.
     struct Slot {
         uint32_t w[K + 1];
-        uint32_t xw, sw;
     };
-    auto load = [&](Slot& sl, const Cursor& q) {
-        g1_load<K>(sl.w, q.p, lk);
-        const int blk = q.tr >> 3;
-        sl.xw = reinterpret_cast<const uint32_t*>(a.x + blk * 128)[lane];
-        sl.sw = reinterpret_cast<const uint32_t*>(sh(q.s).suh + blk * 128)[lane];
-    };
+    auto load = [&](Slot& sl, const Cursor& q) { g1_load<K>(sl.w, q.p, lk); };
     Cursor pf = cursor_at(ub + lo), cu = pf;
     int jpf = 0;
     auto next_pf = [&]() -> const Cursor& {
@@ -251,55 +255,82 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     }
 
     // ---- this workgroup's segments: S_first .. S_first + nseg - 1
-    const int s_first = g1_shard_of_unit<ONE>(a, ub);
+    const int s_first = g1_shard_of_unit<ONE>(a, sht, ub);
     const int S_first = sh(s_first).sbeg + g1_div(ub - sh(s_first).ubeg, a.dntr);
     const int nseg = [&] {
         const int u = ub + L - 1;
-        const int s = g1_shard_of_unit<ONE>(a, u);
+        const int s = g1_shard_of_unit<ONE>(a, sht, u);
         return sh(s).sbeg + g1_div(u - sh(s).ubeg, a.dntr) - S_first + 1;
     }();
-    // LDS: red[nseg][G1_NW][128] fp32 partial rows | last[nseg] flags
+    // The range's 128-input blocks in the order its units meet them ("occurrences"): the
+    // first segment's tile rows tr0 .. tre0 (blocks tr0 / 8 .. tre0 / 8), then every later
+    // segment from tile row 0 on (ntr / 8 blocks each, the last one possibly fewer).
+    // Occurrence of unit (segment S_first + k, tile row tr): see occ_of.
+    const int tr0 = ub - sh(s_first).ubeg - (S_first - sh(s_first).sbeg) * ntr;
+    const int nbpc = ntr >> 3;
+    const int nb0 = (min(ntr - 1, tr0 + L - 1) >> 3) - (tr0 >> 3) + 1;
+    auto occ_of = [&](int k, int tr) { return k == 0 ? (tr >> 3) - (tr0 >> 3) : nb0 + (k - 1) * nbpc + (tr >> 3); };
+    const int nocc = [&] {
+        const int u = ub + L - 1;
+        const int s = g1_shard_of_unit<ONE>(a, sht, u);
+        const int rel = u - sh(s).ubeg;
+        const int cg = g1_div(rel, a.dntr);
+        return occ_of(sh(s).sbeg + cg - S_first, rel - cg * ntr) + 1;
+    }();
+
+    // LDS: red[nseg][G1_NW][128] fp32 partial rows | act[nocc][64] fp16 pairs | last[nseg]
     float* red = reinterpret_cast<float*>(lds);
-    int* last = reinterpret_cast<int*>(red + nseg * G1_NW * 128);
+    uint32_t* act = reinterpret_cast<uint32_t*>(red + nseg * G1_NW * 128);
+    int* last = reinterpret_cast<int*>(act + nocc * 64);
     for (int k = 0; k < nseg; k++)
         *reinterpret_cast<float2*>(red + (k * G1_NW + wave) * 128 + 2 * lane) = float2{0.f, 0.f};
     const Dot2Consts kc = dot2_consts();
 
+    // Activations, once per workgroup while the first trellis loads are in flight: the waves
+    // share out the occurrences; each transforms its block, fp16(H128(x * suh)) (lane l:
+    // outputs 2l, 2l + 1 = rows 2(l % 8), 2(l % 8) + 1 of the block's tile row l / 8, kept
+    // as an fp16 pair).  A unit of tile row t then reads lane 8t + l % 8's pair and
+    // duplicates each half for the v_dot2c broadcasts.
+    for (int i = wave; i < nocc; i += G1_NW) {
+        int k = 0, blk = (tr0 >> 3) + i;
+        if (i >= nb0) {
+            const int j = i - nb0;
+            k = 1 + g1_div(8 * j, a.dntr);          // j / nbpc
+            blk = j - (k - 1) * nbpc;
+        }
+        const int s = g1_shard_of_seg<ONE>(a, sht, S_first + k);
+        const uint32_t xw = reinterpret_cast<const uint32_t*>(a.x + blk * 128)[lane];
+        const uint32_t sw = reinterpret_cast<const uint32_t*>(sh(s).suh + blk * 128)[lane];
+        float v0 = g1_lo(xw) * g1_lo(sw), v1 = g1_hi(xw) * g1_hi(sw);
+        wave_fwht128(v0, v1);
+        act[i * 64 + lane] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) |
+                             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
+    }
+    __syncthreads();
+
     // ---- main loop.  Scalar bookkeeping (cursor steps, column-group crossings, flushes of a
     // finished segment's sums to the wave's LDS row) sits between units, so each unit's work
     // is one basic block the scheduler can interleave; the loads sit outside every branch,
-    // so the wait before a unit covers only that unit's own loads.
-    //
-    // Activations: when a unit enters a new 128-input block (every 8 units, or at a shard or
-    // column-group change) the wave transforms the block, fp16(H128(x * suh)) across the wave
-    // (lane l: outputs 2l, 2l + 1 = rows 2(l % 8), 2(l % 8) + 1 of tile row l / 8, kept as an
-    // fp16 pair); a unit of tile row t then reads lane 8t + l % 8's pair and duplicates each
-    // half for the v_dot2c broadcasts.
+    // so the wait before a unit covers only that unit's own loads.  The occurrence index
+    // steps whenever a unit starts a block (its tile row a multiple of 8, which includes
+    // every segment start).
     const int o0 = (lane >> 3) * 16 + (lane & 7);
     float y0 = 0.f, y1 = 0.f;
     int cur = cu.S - S_first;
+    int occ = occ_of(cur, cu.tr);
+    const uint32_t* act_lane = act + (lane & 7);
     auto flush = [&](int k) {
         red[(cur * G1_NW + wave) * 128 + o0] = y0;
         red[(cur * G1_NW + wave) * 128 + o0 + 8] = y1;
         y0 = y1 = 0.f;
         cur = k;
     };
-    uint32_t bact = 0;
-    int bkey = -1;                            // (shard, block) of bact
     for (int j = 0; j < n; j += D) {
 #pragma unroll
         for (int d = 0; d < D; d++) {
             if (d == 0 || j + d < n) {
                 if (cu.S - S_first != cur) flush(cu.S - S_first);
-                const int key = (cu.s << 24) | (cu.tr >> 3);
-                if (key != bkey) {
-                    bkey = key;
-                    float v0 = g1_lo(ring[d].xw) * g1_lo(ring[d].sw), v1 = g1_hi(ring[d].xw) * g1_hi(ring[d].sw);
-                    wave_fwht128(v0, v1);
-                    bact = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) |
-                           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
-                }
-                const uint32_t pr = (uint32_t)__builtin_amdgcn_ds_bpermute(((cu.tr & 7) * 8 + (lane & 7)) * 4, (int)bact);
+                const uint32_t pr = act_lane[occ * 64 + (cu.tr & 7) * 8];
                 const uint32_t a0 = __builtin_amdgcn_perm(pr, pr, 0x01000100u);
                 const uint32_t a1 = __builtin_amdgcn_perm(pr, pr, 0x03020302u);
                 chunk_prev_dpp<K>(ring[d].w, first_lane);
@@ -307,7 +338,10 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
                 dot2_chunk<K, CB>(ring[d].w, a0, a1, acc, kc);
                 y0 += acc[0] + acc[1];
                 y1 += acc[2] + acc[3];
-                if (j + d + 1 < n) advance(cu);
+                if (j + d + 1 < n) {
+                    advance(cu);
+                    occ += (cu.tr & 7) == 0;
+                }
             }
             load(ring[d], next_pf());
         }
@@ -318,7 +352,7 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     // ---- per segment: fixed-order sum of the waves; finish here, or via the slots
     auto finish = [&](int k, float v0, float v1) {
         const int S = S_first + k;
-        const int s = g1_shard_of_seg<ONE>(a, S);
+        const int s = g1_shard_of_seg<ONE>(a, sht, S);
         const int cg = S - sh(s).sbeg;
         wave_fwht128(v0, v1);
         const uint32_t sv = reinterpret_cast<const uint32_t*>(sh(s).svh + cg * 128)[lane];
@@ -330,7 +364,7 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     };
     auto contributors = [&](int k, int& g_lo, int& g_hi) {
         const int S = S_first + k;
-        const int s = g1_shard_of_seg<ONE>(a, S);
+        const int s = g1_shard_of_seg<ONE>(a, sht, S);
         const int segU0 = sh(s).ubeg + (S - sh(s).sbeg) * ntr;
         g_lo = g1_wg_of(a, segU0);
         g_hi = g1_wg_of(a, segU0 + ntr - 1);
@@ -411,6 +445,45 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     }
 }
 
+// Eight waves per SIMD need at most 64 VGPRs (measured on MI355X: 68 VGPRs leave room for
+// only 6); the SGPR cap keeps the count well inside what eight waves per SIMD may hold.
+template <int K, int CB, bool ONE>
+__global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8), amdgpu_num_sgpr(74))) void gemv1_kernel(const G1Args a)
+{
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    g1_body<K, CB, ONE>(a.grp, a.sh, blockIdx.x, lds);
+}
+
+// Several groups (different K) in one launch: their start-up and reduction tails overlap
+// instead of following each other.
+template <int CB>
+__global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8), amdgpu_num_sgpr(74))) void gemv1_multi_kernel(const G1Multi)
+{
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    // The argument read in place through the kernel-argument segment pointer: indexing the
+    // by-value parameter with a run-time group would make the compiler copy all of it to
+    // scratch memory first.
+    const G1Multi& mm = *(const G1Multi*)__builtin_amdgcn_kernarg_segment_ptr();
+    int i = 0;
+#pragma unroll
+    for (int j = 1; j < G1_MAXSH; j++)
+        if (j < mm.ngrp && (int)blockIdx.x >= mm.gbeg[j]) i = j;
+    i = __builtin_amdgcn_readfirstlane(i);
+    const G1Group& a = mm.grp[i];
+    const G1Shard* sht = mm.sh + mm.sh0[i];
+    const int g = blockIdx.x - mm.gbeg[i];
+    switch (mm.K[i]) {
+    case 1: g1_body<1, CB, false>(a, sht, g, lds); break;
+    case 2: g1_body<2, CB, false>(a, sht, g, lds); break;
+    case 3: g1_body<3, CB, false>(a, sht, g, lds); break;
+    case 4: g1_body<4, CB, false>(a, sht, g, lds); break;
+    case 5: g1_body<5, CB, false>(a, sht, g, lds); break;
+    case 6: g1_body<6, CB, false>(a, sht, g, lds); break;
+    case 7: g1_body<7, CB, false>(a, sht, g, lds); break;
+    case 8: g1_body<8, CB, false>(a, sht, g, lds); break;
+    }
+}
+
 // ---------------------------------------------------------------- host side
 
 template <int K, int CB>
@@ -454,12 +527,16 @@ static G1Div g1_magic(uint32_t d)
 }
 
 // Dynamic LDS a launch needs: a partial row per wave and a flag for the most segments
-// (shard, column group) a workgroup range of ceil(U / G) units can touch.
+// (shard, column group) a workgroup range of ceil(U / G) units can touch, and a transformed
+// activation block for each 128-input block it can meet (at most ceil(L / 8) + nseg + 1:
+// a piece of a segment meets one block more than its length in blocks when it starts
+// inside a block, and only the first piece can).
 static size_t g1_lds_bytes(int U, int G, int ntr)
 {
     const int L = (U + G - 1) / G;
     const int nseg = (L - 1 + ntr - 1) / ntr + 1;
-    return (size_t)nseg * (G1_NW * 128 * sizeof(float) + 4);
+    const int nocc = (L + 7) / 8 + nseg + 1;
+    return (size_t)nseg * (G1_NW * 128 * sizeof(float) + 4) + (size_t)nocc * 64 * sizeof(uint32_t);
 }
 
 // Per-shard share of the workspace after the counter area: slot rows for up to G1_GMAX
@@ -470,72 +547,159 @@ size_t gemv1_slot_bytes(int ic, int oc)
     return (size_t)(G1_GMAX + oc / 128) * 128 * sizeof(float);
 }
 
+// Units per workgroup the launch aims for: fewer, longer ranges cut the cross-workgroup
+// reduction (fewer contributors per column group) and the per-wave start-up, while a
+// launch still spreads over up to G1_WG_PER_CU workgroups per CU.  Measured on MI355X
+// over the 27B projection shapes: 32 is best or within 3% of best for each.
+constexpr int G1_UNITS_PER_WG = 32;
+
+// Fills one group from shards[idx[0..n-1]] (same K and codebook) into table entries
+// tab[0..n-1]; returns its unit count.
+static long g1_group(G1Group& grp, G1Shard* tab, const GemvShard* shards, const int* idx, int n, const uint16_t* A,
+                     int ntr)
+{
+    grp = G1Group{};
+    grp.x = A;
+    grp.ntr = ntr;
+    grp.nshards = n;
+    long U = 0;
+    int nsegs = 0;
+    for (int j = 0; j < n; j++) {
+        const GemvShard& d = shards[idx[j]];
+        G1Shard& e = tab[j];
+        e.trellis = d.trellis;
+        e.suh = d.suh;
+        e.svh = d.svh;
+        e.C = d.C;
+        e.ubeg = (int)U;
+        e.sbeg = nsegs;
+        e.oc16 = d.oc / 16;
+        e.ncg = d.oc / 128;
+        U += (long)(d.oc / 128) * ntr;
+        nsegs += d.oc / 128;
+    }
+    grp.nsegs = nsegs;
+    return U;
+}
+
+// Workgroup split of a group of U units into G ranges, and its share of counters and slots.
+static int g1_place(G1Group& grp, long U, int G, uint32_t* counters, int& cbase, int max_counters, char* slots,
+                    size_t& sbase, size_t slot_bytes)
+{
+    if (U > (1L << 30))
+        return set_error(EXL3_ERR_ARG, "exl3_gemv: %ld tile-row units in one launch (limit 2^30)", U);
+    if (cbase + grp.nsegs > max_counters)
+        return set_error(EXL3_ERR_ARG, "exl3_gemv: %d column groups exceed the %d segment counters",
+                         cbase + grp.nsegs, max_counters);
+    const size_t need = (size_t)(G + grp.nsegs) * 128 * sizeof(float);
+    if (sbase + need > slot_bytes)
+        return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: slot area of %zu bytes, %zu needed", slot_bytes,
+                         sbase + need);
+    grp.U = (int)U;
+    grp.G = G;
+    grp.q = (int)(U / G);
+    grp.r = (int)(U % G);
+    // divisors are >= 8 (ntr = ic / 16 with ic >= 128; G <= U / 8), as g1_div requires
+    grp.dntr = g1_magic((uint32_t)grp.ntr);
+    grp.dq = g1_magic((uint32_t)grp.q);
+    grp.dq1 = g1_magic((uint32_t)grp.q + 1);
+    grp.counters = counters + cbase;
+    grp.slots = reinterpret_cast<float*>(slots + sbase);
+    cbase += grp.nsegs;
+    sbase += need;
+    return EXL3_OK;
+}
+
+static int g1_launch(const void* fn, void* arg, int G, size_t lds, hipStream_t stream)
+{
+    if (lds > 64 * 1024) {
+        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        (void)hipGetLastError();
+    }
+    void* kargs[] = {arg};
+    hipLaunchKernel(fn, dim3(G), dim3(64 * G1_NW), kargs, lds, stream);
+    return check_launch("exl3_gemv (batch 1)");
+}
+
+// Batch 1: the shards are grouped by (K, codebook), at most G1_MAXSH shards a group.  A
+// launch takes whole groups of one codebook, at most G1_MAXSH shards in all: one group is
+// a gemv1_kernel launch, several share a gemv1_multi_kernel launch with their workgroup
+// counts scaled to the resident limit together.
 int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint32_t* counters, int max_counters,
                    char* slots, size_t slot_bytes, hipStream_t stream)
 {
     const int ic = shards[0].ic;
     const int ntr = ic / 16;
+    const int gmax = std::min(G1_GMAX, G1_WG_PER_CU * g1_cu_count());
+    auto g_of = [&](long U) { return (int)std::min<long>(gmax, std::max<long>(1, U / G1_UNITS_PER_WG)); };
 
-    bool done[EXL3_MAX_SHARDS] = {false};
+    // groups: shard indices by (codebook, K) in first-seen order, split every G1_MAXSH shards
+    constexpr int MAXG = EXL3_MAX_SHARDS;
+    int gidx[MAXG][G1_MAXSH], gn[MAXG] = {0}, gK[MAXG], gcb[MAXG], ng = 0;
+    for (int i = 0; i < nshards; i++) {
+        if (shards[i].K < 1 || shards[i].K > 8)
+            return set_error(EXL3_ERR_ARG, "exl3_gemv: K=%d is not in 1..8", shards[i].K);
+        int j = ng - 1;
+        while (j >= 0 && !(gK[j] == shards[i].K && gcb[j] == shards[i].cb && gn[j] < G1_MAXSH)) j--;
+        if (j < 0) {
+            j = ng++;
+            gK[j] = shards[i].K;
+            gcb[j] = shards[i].cb;
+        }
+        gidx[j][gn[j]++] = i;
+    }
+
     int cbase = 0;
     size_t sbase = 0;
-    const int gmax = std::min(G1_GMAX, G1_WG_PER_CU * g1_cu_count());
-    for (int i = 0; i < nshards; i++) {
-        if (done[i]) continue;
-        G1Args args = {};
-        args.x = A;
-        args.ntr = ntr;
-        long U = 0;
-        int nsegs = 0;
-        for (int s = i; s < nshards && args.nshards < G1_MAXSH; s++) {
-            if (done[s] || shards[s].K != shards[i].K || shards[s].cb != shards[i].cb) continue;
-            const GemvShard& d = shards[s];
-            G1Shard& e = args.sh[args.nshards++];
-            e.trellis = d.trellis;
-            e.suh = d.suh;
-            e.svh = d.svh;
-            e.C = d.C;
-            e.ubeg = (int)U;
-            e.sbeg = nsegs;
-            e.oc16 = d.oc / 16;
-            e.ncg = d.oc / 128;
-            U += (long)(d.oc / 128) * ntr;
-            nsegs += d.oc / 128;
-            done[s] = true;
+    bool done[MAXG] = {false};
+    for (int j0 = 0; j0 < ng; j0++) {
+        if (done[j0]) continue;
+        // this launch: group j0 and the following groups of its codebook while they fit
+        int sel[G1_MAXSH], ns = 0, nsh = 0;
+        for (int j = j0; j < ng; j++)
+            if (!done[j] && gcb[j] == gcb[j0] && nsh + gn[j] <= G1_MAXSH) {
+                sel[ns++] = j;
+                nsh += gn[j];
+                done[j] = true;
+            }
+        const int cb = gcb[j0];
+        if (ns == 1) {
+            G1Args args = {};
+            const long U = g1_group(args.grp, args.sh, shards, gidx[j0], gn[j0], A, ntr);
+            const int G = g_of(U);
+            int rc = g1_place(args.grp, U, G, counters, cbase, max_counters, slots, sbase, slot_bytes);
+            if (rc != EXL3_OK) return rc;
+            rc = g1_launch(g1_fn_kcb(gK[j0], cb, gn[j0] == 1), &args, G, g1_lds_bytes((int)U, G, ntr), stream);
+            if (rc != EXL3_OK) return rc;
+            continue;
         }
-        if (U > (1L << 30))
-            return set_error(EXL3_ERR_ARG, "exl3_gemv: %ld tile-row units in one launch (limit 2^30)", U);
-        if (cbase + nsegs > max_counters)
-            return set_error(EXL3_ERR_ARG, "exl3_gemv: %d column groups exceed the %d segment counters",
-                             cbase + nsegs, max_counters);
-        const int G = (int)std::min<long>(gmax, std::max<long>(1, U / G1_NW));
-        const size_t lds = g1_lds_bytes((int)U, G, ntr);
-        const size_t need = (size_t)(G + nsegs) * 128 * sizeof(float);
-        if (sbase + need > slot_bytes)
-            return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: slot area of %zu bytes, %zu needed", slot_bytes,
-                             sbase + need);
-        args.U = (int)U;
-        args.G = G;
-        args.q = (int)(U / G);
-        args.r = (int)(U % G);
-        // divisors are >= 8 (ntr = ic / 16 with ic >= 128; G <= U / 8), as g1_div requires
-        args.dntr = g1_magic((uint32_t)ntr);
-        args.dq = g1_magic((uint32_t)args.q);
-        args.dq1 = g1_magic((uint32_t)args.q + 1);
-        args.nsegs = nsegs;
-        args.counters = counters + cbase;
-        args.slots = reinterpret_cast<float*>(slots + sbase);
-        cbase += nsegs;
-        sbase += need;
-        const void* fn = g1_fn_kcb(shards[i].K, shards[i].cb, args.nshards == 1);
-        if (!fn) return set_error(EXL3_ERR_ARG, "exl3_gemv: K=%d is not in 1..8", shards[i].K);
-        if (lds > 64 * 1024) {
-            hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-            (void)hipGetLastError();
+        G1Multi m = {};
+        long U[G1_MAXSH], Gsum = 0;
+        int G[G1_MAXSH], sh0 = 0;
+        for (int t = 0; t < ns; t++) {
+            const int j = sel[t];
+            m.sh0[t] = sh0;
+            m.K[t] = gK[j];
+            U[t] = g1_group(m.grp[t], m.sh + sh0, shards, gidx[j], gn[j], A, ntr);
+            sh0 += gn[j];
+            G[t] = g_of(U[t]);
+            Gsum += G[t];
         }
-        void* kargs[] = {&args};
-        hipLaunchKernel(fn, dim3(G), dim3(64 * G1_NW), kargs, lds, stream);
-        const int rc = check_launch("exl3_gemv (batch 1)");
+        if (Gsum > gmax)   // share the resident workgroups in proportion to the groups' sizes
+            for (int t = 0; t < ns; t++) G[t] = std::max(1, (int)((long)G[t] * gmax / Gsum));
+        size_t lds = 0;
+        int gb = 0;
+        for (int t = 0; t < ns; t++) {
+            const int rc = g1_place(m.grp[t], U[t], G[t], counters, cbase, max_counters, slots, sbase, slot_bytes);
+            if (rc != EXL3_OK) return rc;
+            m.gbeg[t] = gb;
+            gb += G[t];
+            lds = std::max(lds, g1_lds_bytes((int)U[t], G[t], ntr));
+        }
+        m.ngrp = ns;
+        const void* fn = cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG>)
+                                      : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST>);
+        const int rc = g1_launch(fn, &m, gb, lds, stream);
         if (rc != EXL3_OK) return rc;
     }
     return EXL3_OK;

@@ -164,6 +164,39 @@ def test_gemv_grouped_config2(native, oracle, rows):
             col += l["oc"]
 
 
+@pytest.mark.parametrize("ic,ocs,K", [(128, [131200], 2), (256, [384, 128, 640], 3), (384, [1152], 5),
+                                      (2048, [128], 4), (256, [2048, 2048], 4), (640, [128, 256, 128], 6)])
+def test_gemv1_workgroup_ranges(native, oracle, ic, ocs, K):
+    """Batch 1 with workgroup ranges that span several column groups and shards, start
+    inside a 128-input block, or cover a whole launch."""
+    x = syn.activations(1, ic, torch.Generator().manual_seed(ic + K))
+    lins = [syn.linear(ic, oc, K, seed=300 + i) for i, oc in enumerate(ocs)]
+    shards = [dict(to_gpu(l), codebook=0) for l in lins]
+    y = native.gemv_grouped(x.to(dev()), shards)
+    col = 0
+    for l in lins:
+        check_linear_out(y[:, col:col + l["oc"]], x, l, 0, oracle)
+        col += l["oc"]
+
+
+@pytest.mark.parametrize("rows", [1, 3, 9])
+def test_gemv_grouped_mixed_K_and_codebooks(native, oracle, rows):
+    """Shards of several K (interleaved, so a group is not a contiguous run of shards) and
+    both codebooks in one grouped call; at batch 1 each codebook's groups share a launch."""
+    spec = [(384, 3, 0), (256, 5, 0), (128, 3, 1), (640, 2, 0), (256, 3, 0), (128, 6, 1), (384, 5, 0)]
+    x = syn.activations(rows, 768, torch.Generator().manual_seed(40 + rows))
+    lins = [syn.linear(768, oc, K, seed=400 + i) for i, (oc, K, _) in enumerate(spec)]
+    shards = [dict(to_gpu(l), codebook=cb) for l, (_, _, cb) in zip(lins, spec)]
+    y = native.gemv_grouped(x.to(dev()), shards)
+    ys = [native.gemv_grouped(x.to(dev()), shards) for _ in range(2)]
+    col = 0
+    for l, (_, _, cb) in zip(lins, spec):
+        check_linear_out(y[:, col:col + l["oc"]], x, l, cb, oracle)
+        col += l["oc"]
+    for yy in ys:
+        assert torch.equal(yy, y)
+
+
 # ---------------------------------------------------------------- GEMM
 
 @pytest.mark.parametrize("rows", [17, 64, 100, 144, 300])
