@@ -28,6 +28,7 @@ embedding gather of one batch-1 token as one HIP graph, replayed (attention excl
 
     python bench.py --workload config2   # grouped qkv / gate_up GEMVs at batch 1, 4, 16
     python bench.py --workload config3   # M=2048 prefill GEMM (TFLOP/s, MFMA share) + reconstruct
+    python bench.py --workload config4   # the 64-layer batch-1 linear stack alone (tok/s-equivalent)
 print their own JSON line instead of the headline line.
 """
 from __future__ import annotations
@@ -414,9 +415,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-K", type=int, default=0, help="time a single K (profiling runs)")
     ap.add_argument("--copy-calib", action="store_true", help="run the counter-calibration copy and exit")
-    ap.add_argument("--workload", default="config1", choices=("config1", "config2", "config3"),
-                    help="config1 = the headline line (+ the config-4 stack); config2/config3 print "
-                         "their own measurement line")
+    ap.add_argument("--workload", default="config1", choices=("config1", "config2", "config3", "config4"),
+                    help="config1 = the headline line (+ the config-4 stack); config2/config3/config4 "
+                         "print their own measurement line")
     ap.add_argument("--no-stack", action="store_true", help="skip the config-4 stack measurement")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -427,9 +428,10 @@ def main():
     if args.copy_calib:
         copy_calib(args)
         return
-    if args.workload in ("config2", "config3"):
+    if args.workload in ("config2", "config3", "config4"):
         import torch
-        res = config2_bench(args.steps * 5) if args.workload == "config2" else config3_bench(args.steps)
+        res = (config2_bench(args.steps * 5) if args.workload == "config2" else
+               config3_bench(args.steps) if args.workload == "config3" else stack_bench(args.steps))
         print(json.dumps({"workload": args.workload, "results": res,
                           "device": torch.cuda.get_device_name(0)}), flush=True)
         return

@@ -169,6 +169,34 @@ __device__ __forceinline__ void g1_load(uint32_t (&w)[K + 1], const uint32_t* __
     }
 }
 
+// One lane's chunk (32 positions) multiplied into its two output columns with
+// v_mfma_f32_4x4x4_16b_f16: the activations go in A (the same for every lane, so each
+// 4-row block of A repeats them) and the lane's masked codebook words in B, each word's two
+// fp16 halves as two k-slots against one activation twice -- so the weight's fp16 half-sum
+// is never rounded, and block b's column n (lane 4b + n) collects only that lane's products.
+// MFMA J takes positions q0 = 8m + 2p + 4h and q0 + 1 (m = J / 4, p = J / 2 % 2, h = J % 2):
+// rows 2m + 8p and 2m + 8p + 1 of the tile row (act16 holds the 16 rows as duplicated fp16
+// pairs), output column half h (acc[h]).
+template <int K, int CB, int J>
+__device__ __forceinline__ void g1_mfma_pair(const uint32_t (&w)[K + 1], const uint32_t (&act16)[16], f32x4 (&acc)[2],
+                                             const Dot2Consts& kc)
+{
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+    constexpr int m = J / 4, p = (J / 2) % 2, h = J % 2;
+    constexpr int q0 = 8 * m + 2 * p + 4 * h;
+    const u2 bv = {dot2_word<K, CB, q0>(w, kc), dot2_word<K, CB, q0 + 1>(w, kc)};
+    const u2 av = {act16[2 * m + 8 * p], act16[2 * m + 8 * p + 1]};
+    acc[h] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(h4, av), __builtin_bit_cast(h4, bv), acc[h], 0, 0, 0);
+}
+
+template <int K, int CB, int... Js>
+__device__ __forceinline__ void g1_mfma_chunk(const uint32_t (&w)[K + 1], const uint32_t (&act16)[16], f32x4 (&acc)[2],
+                                              const Dot2Consts& kc, std::integer_sequence<int, Js...>)
+{
+    (g1_mfma_pair<K, CB, Js>(w, act16, acc, kc), ...);
+}
+
 __device__ __forceinline__ uint32_t g1_dup(float v)
 {
     const uint32_t h = __builtin_bit_cast(uint16_t, (_Float16)v);
@@ -278,19 +306,19 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         return occ_of(sh(s).sbeg + cg - S_first, rel - cg * ntr) + 1;
     }();
 
-    // LDS: red[nseg][G1_NW][128] fp32 partial rows | act[nocc][64] fp16 pairs | last[nseg]
+    // LDS: red[nseg][G1_NW][128] fp32 partial rows | act[nocc][8][16] duplicated fp16
+    // activations | last[nseg]
     float* red = reinterpret_cast<float*>(lds);
     uint32_t* act = reinterpret_cast<uint32_t*>(red + nseg * G1_NW * 128);
-    int* last = reinterpret_cast<int*>(act + nocc * 64);
+    int* last = reinterpret_cast<int*>(act + nocc * 128);
     for (int k = 0; k < nseg; k++)
         *reinterpret_cast<float2*>(red + (k * G1_NW + wave) * 128 + 2 * lane) = float2{0.f, 0.f};
     const Dot2Consts kc = dot2_consts();
 
     // Activations, once per workgroup while the first trellis loads are in flight: the waves
     // share out the occurrences; each transforms its block, fp16(H128(x * suh)) (lane l:
-    // outputs 2l, 2l + 1 = rows 2(l % 8), 2(l % 8) + 1 of the block's tile row l / 8, kept
-    // as an fp16 pair).  A unit of tile row t then reads lane 8t + l % 8's pair and
-    // duplicates each half for the v_dot2c broadcasts.
+    // outputs 2l, 2l + 1 = rows 2(l % 8), 2(l % 8) + 1 of the block's tile row l / 8) and
+    // stores each output as a duplicated fp16 pair: act[occurrence][tile row][row].
     for (int i = wave; i < nocc; i += G1_NW) {
         int k = 0, blk = (tr0 >> 3) + i;
         if (i >= nb0) {
@@ -303,8 +331,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         const uint32_t sw = reinterpret_cast<const uint32_t*>(sh(s).suh + blk * 128)[lane];
         float v0 = g1_lo(xw) * g1_lo(sw), v1 = g1_hi(xw) * g1_hi(sw);
         wave_fwht128(v0, v1);
-        act[i * 64 + lane] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) |
-                             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
+        *reinterpret_cast<uint2*>(act + (i * 8 + (lane >> 3)) * 16 + 2 * (lane & 7)) = uint2{g1_dup(v0), g1_dup(v1)};
     }
     __syncthreads();
 
@@ -315,14 +342,13 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     // steps whenever a unit starts a block (its tile row a multiple of 8, which includes
     // every segment start).
     const int o0 = (lane >> 3) * 16 + (lane & 7);
-    float y0 = 0.f, y1 = 0.f;
+    f32x4 yacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};   // columns o0, o0 + 8 (4 equal copies)
     int cur = cu.S - S_first;
     int occ = occ_of(cur, cu.tr);
-    const uint32_t* act_lane = act + (lane & 7);
     auto flush = [&](int k) {
-        red[(cur * G1_NW + wave) * 128 + o0] = y0;
-        red[(cur * G1_NW + wave) * 128 + o0 + 8] = y1;
-        y0 = y1 = 0.f;
+        red[(cur * G1_NW + wave) * 128 + o0] = yacc[0].x;
+        red[(cur * G1_NW + wave) * 128 + o0 + 8] = yacc[1].x;
+        yacc[0] = yacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
         cur = k;
     };
     for (int j = 0; j < n; j += D) {
@@ -330,14 +356,15 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         for (int d = 0; d < D; d++) {
             if (d == 0 || j + d < n) {
                 if (cu.S - S_first != cur) flush(cu.S - S_first);
-                const uint32_t pr = act_lane[occ * 64 + (cu.tr & 7) * 8];
-                const uint32_t a0 = __builtin_amdgcn_perm(pr, pr, 0x01000100u);
-                const uint32_t a1 = __builtin_amdgcn_perm(pr, pr, 0x03020302u);
+                const uint4* ap = reinterpret_cast<const uint4*>(act + (occ * 8 + (cu.tr & 7)) * 16);
+                uint32_t act16[16];
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const uint4 t = ap[v];
+                    act16[4 * v] = t.x; act16[4 * v + 1] = t.y; act16[4 * v + 2] = t.z; act16[4 * v + 3] = t.w;
+                }
                 chunk_prev_dpp<K>(ring[d].w, first_lane);
-                float acc[4] = {0.f, 0.f, 0.f, 0.f};
-                dot2_chunk<K, CB>(ring[d].w, a0, a1, acc, kc);
-                y0 += acc[0] + acc[1];
-                y1 += acc[2] + acc[3];
+                g1_mfma_chunk<K, CB>(ring[d].w, act16, yacc, kc, std::make_integer_sequence<int, 16>{});
                 if (j + d + 1 < n) {
                     advance(cu);
                     occ += (cu.tr & 7) == 0;
@@ -536,7 +563,7 @@ static size_t g1_lds_bytes(int U, int G, int ntr)
     const int L = (U + G - 1) / G;
     const int nseg = (L - 1 + ntr - 1) / ntr + 1;
     const int nocc = (L + 7) / 8 + nseg + 1;
-    return (size_t)nseg * (G1_NW * 128 * sizeof(float) + 4) + (size_t)nocc * 64 * sizeof(uint32_t);
+    return (size_t)nseg * (G1_NW * 128 * sizeof(float) + 4) + (size_t)nocc * 128 * sizeof(uint32_t);
 }
 
 // Per-shard share of the workspace after the counter area: slot rows for up to G1_GMAX
