@@ -47,8 +47,15 @@ struct SkCfg<16> { static constexpr int WM = 1, WN = 8, MB = 1, NB = 2; };
 
 template <int BM>
 constexpr int sk_acc() { return SkCfg<BM>::MB * SkCfg<BM>::NB * 4; }   // fp32 accumulators per lane
+// LDS of a launch: the A and B tiles of one K-step, twice for BM = 256 (the tiles of step
+// s + 1 are written while the MFMAs read those of step s), once for BM = 16 (three
+// workgroups per CU).
 template <int BM>
-constexpr int sk_lds() { return (BM + SK_BN) * SK_LD * 2; }             // A + B tiles, bytes
+constexpr int sk_nbuf() { return BM == 256 ? 2 : 1; }
+template <int BM>
+constexpr int sk_buf() { return (BM + SK_BN) * SK_LD; }                   // halves per A + B buffer
+template <int BM>
+constexpr int sk_lds() { return sk_nbuf<BM>() * sk_buf<BM>() * 2; }      // bytes
 
 struct SkShard {
     const uint16_t* Ah;        // (rows, ic) fp16, fp16(H(A * suh)) of this shard
@@ -197,8 +204,8 @@ void gemm_sk_kernel(const SkArgs a)
     using Cfg = SkCfg<BM>;
     constexpr int MB = Cfg::MB, NB = Cfg::NB, ACC = sk_acc<BM>();
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-    _Float16* As = reinterpret_cast<_Float16*>(lds);
-    _Float16* Bs = As + BM * SK_LD;
+    auto As = [&](int b) { return reinterpret_cast<_Float16*>(lds) + b * sk_buf<BM>(); };
+    auto Bs = [&](int b) { return reinterpret_cast<_Float16*>(lds) + b * sk_buf<BM>() + BM * SK_LD; };
 
     const int g = sk_logical(blockIdx.x);
     const int tid = threadIdx.x;
@@ -251,17 +258,40 @@ void gemm_sk_kernel(const SkArgs a)
             const int ti = 4 * s + (btile >> 4);
             sk_load<K>(w, S.trellis + ((long)ti * tc + (bok ? btn : 0)) * (8 * K) + c * K, bok);
         };
-        auto store_step = [&]() {
+        // the registers of a K-step into LDS buffer b: A as loaded, B decoded
+        auto store_step = [&](int b) {
+            _Float16* as = As(b);
+            _Float16* bs = Bs(b);
 #pragma unroll
             for (int p = 0; p < AP; p++)
-                if (aload) *reinterpret_cast<uint4*>(As + (64 * p + arow) * SK_LD + aseg * 8) = areg[p];
+                if (aload) *reinterpret_cast<uint4*>(as + (64 * p + arow) * SK_LD + aseg * 8) = areg[p];
             chunk_prev_dpp<K>(w, first_lane);
             uint4 o[4];
             sk_decode<K, CB>(w, kc, o);
-            *reinterpret_cast<uint4*>(Bs + bn0 * SK_LD + bk0) = o[0];
-            *reinterpret_cast<uint4*>(Bs + bn0 * SK_LD + bk0 + 8) = o[1];
-            *reinterpret_cast<uint4*>(Bs + (bn0 + 8) * SK_LD + bk0) = o[2];
-            *reinterpret_cast<uint4*>(Bs + (bn0 + 8) * SK_LD + bk0 + 8) = o[3];
+            *reinterpret_cast<uint4*>(bs + bn0 * SK_LD + bk0) = o[0];
+            *reinterpret_cast<uint4*>(bs + bn0 * SK_LD + bk0 + 8) = o[1];
+            *reinterpret_cast<uint4*>(bs + (bn0 + 8) * SK_LD + bk0) = o[2];
+            *reinterpret_cast<uint4*>(bs + (bn0 + 8) * SK_LD + bk0 + 8) = o[3];
+        };
+        // the MFMAs of one K-step from LDS buffer b
+        auto mfma_step = [&](int b) {
+            const _Float16* as = As(b);
+            const _Float16* bs = Bs(b);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                f16x8 bf[NB];
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+                    bf[nb] = *reinterpret_cast<const f16x8*>(bs + (NB * 16 * wn + 16 * nb + (lane & 15)) * SK_LD +
+                                                             32 * h + 8 * (lane >> 4));
+#pragma unroll
+                for (int mb = 0; mb < MB; mb++) {
+                    const f16x8 af = *reinterpret_cast<const f16x8*>(as + (MB * 16 * wm + 16 * mb + (lane & 15)) * SK_LD +
+                                                                     32 * h + 8 * (lane >> 4));
+#pragma unroll
+                    for (int nb = 0; nb < NB; nb++) acc[mb][nb] = mfma16x16x32(af, bf[nb], acc[mb][nb]);
+                }
+            }
         };
 
 #pragma unroll
@@ -270,25 +300,40 @@ void gemm_sk_kernel(const SkArgs a)
             for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
         load_step(s0);
-        for (int s = s0; s < s1; s++) {
-            __syncthreads();                  // the previous step's MFMAs are done with LDS
-            store_step();
+        if constexpr (sk_nbuf<BM>() == 2) {
+            // Software pipeline over two LDS buffers, one barrier per K-step: during step s the
+            // MFMAs read buffer (s - s0) % 2 while the step s + 1 tiles (loaded into registers
+            // a step earlier) are decoded into the other buffer and step s + 2 is loaded.  The
+            // step is one basic block (the last steps re-decode and re-load in-bounds data that
+            // is never read), so the scheduler can issue the decode's VALU work between the
+            // MFMAs, which run on the matrix pipe meanwhile.
+            store_step(0);
+            load_step(min(s0 + 1, s1 - 1));
             __syncthreads();
-            if (s + 1 < s1) load_step(s + 1);
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                f16x8 bf[NB];
-#pragma unroll
-                for (int nb = 0; nb < NB; nb++)
-                    bf[nb] = *reinterpret_cast<const f16x8*>(Bs + (NB * 16 * wn + 16 * nb + (lane & 15)) * SK_LD +
-                                                             32 * h + 8 * (lane >> 4));
-#pragma unroll
-                for (int mb = 0; mb < MB; mb++) {
-                    const f16x8 af = *reinterpret_cast<const f16x8*>(As + (MB * 16 * wm + 16 * mb + (lane & 15)) * SK_LD +
-                                                                     32 * h + 8 * (lane >> 4));
-#pragma unroll
-                    for (int nb = 0; nb < NB; nb++) acc[mb][nb] = mfma16x16x32(af, bf[nb], acc[mb][nb]);
+            if (wave < SK_WAVES / 2) {
+                for (int s = s0; s < s1; s++) {
+                    const int b = (s - s0) & 1;
+                    mfma_step(b);
+                    store_step(b ^ 1);
+                    load_step(min(s + 2, s1 - 1));
+                    __syncthreads();          // buffer b ^ 1 is complete; buffer b is free
                 }
+            } else {
+                for (int s = s0; s < s1; s++) {
+                    const int b = (s - s0) & 1;
+                    store_step(b ^ 1);
+                    load_step(min(s + 2, s1 - 1));
+                    mfma_step(b);
+                    __syncthreads();          // buffer b ^ 1 is complete; buffer b is free
+                }
+            }
+        } else {
+            for (int s = s0; s < s1; s++) {
+                __syncthreads();              // the previous step's MFMAs are done with LDS
+                store_step(0);
+                __syncthreads();
+                if (s + 1 < s1) load_step(s + 1);
+                mfma_step(0);
             }
         }
         u += s1 - s0;
