@@ -34,9 +34,10 @@ struct GemvShard {
 // counters it uses).  Partial-sum buffers of all GEMV paths start after it.
 constexpr size_t GEMV_COUNTER_BYTES = 16384;
 size_t gemv_workspace_bytes(int rows, int ic, int oc);
-size_t gemv1_slot_bytes(int ic, int oc);
-int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint32_t* counters, int max_counters,
-                   char* slots, size_t slot_bytes, hipStream_t stream);
+size_t gemv1_slot_bytes(int ic, int oc, int rows);
+bool gemv1_rows_fit(const GemvShard* shards, int nshards);
+int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, uint32_t* counters,
+                   int max_counters, char* slots, size_t slot_bytes, hipStream_t stream);
 int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows,
                   void* workspace, size_t ws_bytes, hipStream_t stream);
 size_t gemm_workspace_bytes(int rows, int ic, int oc);

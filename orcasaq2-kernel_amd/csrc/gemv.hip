@@ -3,8 +3,9 @@
 // with W_q decoded from the packed trellis on the fly and never written anywhere.
 // Replaces exllamav3_ext.exl3_gemm as called at orcasaq2/ops.py:46-49 (rows <= 144 there;
 // this path takes rows <= 16 and the MFMA GEMM takes the rest).  Row counts:
-//   * 1: gemv1.hip (persistent decode with v_dot2c);
-//   * 2..GV_SPLIT_MAX_ROWS: the two kernels below;
+//   * 1: gemv1.hip (persistent decode, MFMA multiply-accumulate);
+//   * 2..GV_SPLIT_MAX_ROWS: gemv1.hip as well where its launch keeps three workgroups per
+//     CU resident (gemv1_rows_fit), else the two kernels below;
 //   * above: gemm_sk.hip with 16-row tiles (decode into LDS once per tile, MFMA from LDS;
 //     the cost hardly depends on the row count).
 //
@@ -73,7 +74,10 @@ static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // Per-shard share of a GEMV workspace (the counter area is added once per call).
 size_t gemv_workspace_bytes(int rows, int ic, int oc)
 {
-    if (rows == 1) return align256(gemv1_slot_bytes(ic, oc));
+    if (rows == 1) return align256(gemv1_slot_bytes(ic, oc, 1));
+    if (rows <= GV_SPLIT_MAX_ROWS)   // either path: the 1..4-row kernel's slots or the split partials
+        return align256(std::max(gemv1_slot_bytes(ic, oc, rows),
+                                 (size_t)gemv_splits(ic, oc) * rows * oc * sizeof(float)));
     if (rows > GV_SPLIT_MAX_ROWS) return align256(gemv_sk_bytes(rows, ic, oc));
     return align256((size_t)gemv_splits(ic, oc) * rows * oc * sizeof(float));
 }
@@ -300,8 +304,8 @@ int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int r
                          offs[nshards]);
 
     char* ws = static_cast<char*>(workspace);
-    if (rows == 1)
-        return gemv1_dispatch(A, shards, nshards, reinterpret_cast<uint32_t*>(ws),
+    if (rows == 1 || (rows <= GV_SPLIT_MAX_ROWS && gemv1_rows_fit(shards, nshards)))
+        return gemv1_dispatch(A, shards, nshards, rows, reinterpret_cast<uint32_t*>(ws),
                               (int)(GEMV_COUNTER_BYTES / sizeof(uint32_t)), ws + GEMV_COUNTER_BYTES,
                               offs[nshards] - GEMV_COUNTER_BYTES, stream);
     if (rows > GV_SPLIT_MAX_ROWS)

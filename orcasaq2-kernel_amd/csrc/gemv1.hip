@@ -1,8 +1,9 @@
-// Fused EXL3 decode-GEMV for one activation row (batch-1 decode):
-//   y (oc) = fp16( H( fp16(H(x * suh)) . W_q ) * svh )
+// Fused EXL3 decode-GEMV for one to four activation rows (batch-1..4 decode):
+//   y_r (oc) = fp16( H( fp16(H(x_r * suh)) . W_q ) * svh ),  r < nrows
 // with W_q decoded from the packed trellis in registers and never stored.  Replaces
-// exllamav3_ext.exl3_gemm as called at orcasaq2/ops.py:46-49 for rows == 1 (the other row
-// counts take gemv.hip's MFMA kernels).
+// exllamav3_ext.exl3_gemm as called at orcasaq2/ops.py:46-49 for rows <= 4 (rows 2..4 only
+// where the launch keeps three workgroups per CU resident; gemv.hip's split kernels take
+// the rest, gemm_sk.hip's 16-row tiles take 5..16 rows).
 //
 // Work decomposition.  A *unit* is one tile row of one 128-output column group: 8 tiles
 // side by side, 64 chunks of 32 positions -- one chunk per lane of a wave, the 8 tiles'
@@ -13,17 +14,17 @@
 // *segments* (shard, column group); its eight waves take eight contiguous runs of it.
 //
 // Per wave:
-//   1. issue the loads of its first D units (D = 2..6 by K): the lane's K trellis words and
-//      its x and suh dwords of the unit's 128-input block, so HBM is busy from the start;
+//   1. issue the loads of its first D units (D = 2..6 by K); while they are in flight the
+//      workgroup transforms the activation blocks its range meets, fp16(H128(x_r * suh))
+//      for every row r, into an LDS table of duplicated fp16 pairs;
 //   2. main loop over the run: a unit's data streams through the D-deep register ring.
-//      Entering a new 128-input block (every 8 units), the wave transforms it,
-//      fp16(H128(x * suh)), and keeps the 128 results as one fp16 pair per lane; a unit of
-//      tile row t fetches lane 8t + l % 8's pair (one ds_bpermute) and duplicates each half.
 //      The tail-biting word before a lane's chunk is the previous lane's last word (DPP
 //      rotate within the tile's 8 lanes).  Each position is decoded with an SDWA add (or a
-//      16-bit field for MCG), a v_mul_lo_u32 and a v_bitop3; the masked word meets its
-//      activation in a v_dot2c_f32_f16 whose second operand is broadcast by DPP from the lane
-//      that holds that activation row (both fp16 halves times x, summed in fp32);
+//      16-bit field for MCG), a v_mul_lo_u32 and a v_bitop3; the masked words go into the
+//      B operand of v_mfma_f32_4x4x4_16b_f16 (each word's two fp16 halves as two k-slots
+//      against one activation twice, so lo * x + hi * x is summed in fp32) and the unit's
+//      activations into A: block row i (lane 4b + i) carries activation row i, so one MFMA
+//      serves up to four rows and column j (lane 4b + j) collects lane 4b + j's products;
 //   3. per segment, the waves' partial sums are added in a fixed order through LDS.  If the
 //      segment lies inside this workgroup's range it is finished here; otherwise the
 //      partial goes to this workgroup's slot with agent-coherent stores, and the last of the
@@ -51,7 +52,8 @@ struct G1Shard {
     const uint32_t* trellis;   // (ic/16, oc/16, 8K) u32
     const uint16_t* suh;       // (ic)
     const uint16_t* svh;       // (oc)
-    uint16_t* C;               // (oc) fp16 output
+    uint16_t* C;               // (nrows, ldc) fp16 output, columns [0, oc)
+    long ldc;
     int ubeg;                  // first unit of the shard
     int sbeg;                  // first segment of the shard
     int oc16;                  // tile columns
@@ -75,7 +77,8 @@ __device__ __forceinline__ int g1_div(int x, G1Div d)
 
 // One group of shards with the same K and codebook, decoded by G workgroups.
 struct G1Group {
-    const uint16_t* x;         // (ic) fp16
+    const uint16_t* x;         // (nrows, ic) fp16
+    int nrows;                 // activation rows, 1 .. R of the kernel
     uint32_t* counters;        // one per segment; zero between calls
     float* slots;              // (G + segments) x 128 fp32
     int U, G, ntr, nshards, nsegs;
@@ -206,7 +209,7 @@ __device__ __forceinline__ uint32_t g1_dup(float v)
 // ---------------------------------------------------------------- decode kernel
 
 // Workgroup g of group a (shard table sht) -- the whole kernel body.
-template <int K, int CB, bool ONE>
+template <int K, int CB, bool ONE, int R>
 __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, const int g, uint32_t* lds)
 {
     // shard table entry; a single-shard group (ONE) only ever reads entry 0
@@ -306,19 +309,24 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         return occ_of(sh(s).sbeg + cg - S_first, rel - cg * ntr) + 1;
     }();
 
-    // LDS: red[nseg][G1_NW][128] fp32 partial rows | act[nocc][8][16] duplicated fp16
+    // LDS: red[nseg][G1_NW][R][128] fp32 partial rows | act[nocc][8][R][16] duplicated fp16
     // activations | last[nseg]
     float* red = reinterpret_cast<float*>(lds);
-    uint32_t* act = reinterpret_cast<uint32_t*>(red + nseg * G1_NW * 128);
-    int* last = reinterpret_cast<int*>(act + nocc * 128);
+    uint32_t* act = reinterpret_cast<uint32_t*>(red + nseg * G1_NW * R * 128);
+    int* last = reinterpret_cast<int*>(act + nocc * R * 128);
     for (int k = 0; k < nseg; k++)
-        *reinterpret_cast<float2*>(red + (k * G1_NW + wave) * 128 + 2 * lane) = float2{0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < R; r++)
+            *reinterpret_cast<float2*>(red + ((k * G1_NW + wave) * R + r) * 128 + 2 * lane) = float2{0.f, 0.f};
     const Dot2Consts kc = dot2_consts();
+    const long ic = (long)ntr * 16;
 
     // Activations, once per workgroup while the first trellis loads are in flight: the waves
-    // share out the occurrences; each transforms its block, fp16(H128(x * suh)) (lane l:
-    // outputs 2l, 2l + 1 = rows 2(l % 8), 2(l % 8) + 1 of the block's tile row l / 8) and
-    // stores each output as a duplicated fp16 pair: act[occurrence][tile row][row].
+    // share out the occurrences; each transforms its block of every activation row r,
+    // fp16(H128(x_r * suh)) (lane l: outputs 2l, 2l + 1 = rows 2(l % 8), 2(l % 8) + 1 of the
+    // block's tile row l / 8) and stores each output as a duplicated fp16 pair:
+    // act[occurrence][tile row][r][row].  Rows r >= nrows repeat the last row (their
+    // results are not stored).
     for (int i = wave; i < nocc; i += G1_NW) {
         int k = 0, blk = (tr0 >> 3) + i;
         if (i >= nb0) {
@@ -327,11 +335,15 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
             blk = j - (k - 1) * nbpc;
         }
         const int s = g1_shard_of_seg<ONE>(a, sht, S_first + k);
-        const uint32_t xw = reinterpret_cast<const uint32_t*>(a.x + blk * 128)[lane];
         const uint32_t sw = reinterpret_cast<const uint32_t*>(sh(s).suh + blk * 128)[lane];
-        float v0 = g1_lo(xw) * g1_lo(sw), v1 = g1_hi(xw) * g1_hi(sw);
-        wave_fwht128(v0, v1);
-        *reinterpret_cast<uint2*>(act + (i * 8 + (lane >> 3)) * 16 + 2 * (lane & 7)) = uint2{g1_dup(v0), g1_dup(v1)};
+#pragma unroll 1
+        for (int r = 0; r < R; r++) {
+            const uint32_t xw = reinterpret_cast<const uint32_t*>(a.x + min(r, a.nrows - 1) * ic + blk * 128)[lane];
+            float v0 = g1_lo(xw) * g1_lo(sw), v1 = g1_hi(xw) * g1_hi(sw);
+            wave_fwht128(v0, v1);
+            *reinterpret_cast<uint2*>(act + ((i * 8 + (lane >> 3)) * R + r) * 16 + 2 * (lane & 7)) =
+                uint2{g1_dup(v0), g1_dup(v1)};
+        }
     }
     __syncthreads();
 
@@ -342,12 +354,18 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     // steps whenever a unit starts a block (its tile row a multiple of 8, which includes
     // every segment start).
     const int o0 = (lane >> 3) * 16 + (lane & 7);
-    f32x4 yacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};   // columns o0, o0 + 8 (4 equal copies)
+    // yacc[h][r]: activation row r's sum for column o0 + 8 h (rows r >= R are copies)
+    f32x4 yacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    // the activation row this lane feeds into the MFMAs' A operand (A row = lane % 4)
+    const int arow = R == 1 ? 0 : min(lane & 3, R - 1);
     int cur = cu.S - S_first;
     int occ = occ_of(cur, cu.tr);
     auto flush = [&](int k) {
-        red[(cur * G1_NW + wave) * 128 + o0] = yacc[0].x;
-        red[(cur * G1_NW + wave) * 128 + o0 + 8] = yacc[1].x;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            red[((cur * G1_NW + wave) * R + r) * 128 + o0] = yacc[0][r];
+            red[((cur * G1_NW + wave) * R + r) * 128 + o0 + 8] = yacc[1][r];
+        }
         yacc[0] = yacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
         cur = k;
     };
@@ -356,7 +374,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         for (int d = 0; d < D; d++) {
             if (d == 0 || j + d < n) {
                 if (cu.S - S_first != cur) flush(cu.S - S_first);
-                const uint4* ap = reinterpret_cast<const uint4*>(act + (occ * 8 + (cu.tr & 7)) * 16);
+                const uint4* ap = reinterpret_cast<const uint4*>(act + ((occ * 8 + (cu.tr & 7)) * R + arow) * 16);
                 uint32_t act16[16];
 #pragma unroll
                 for (int v = 0; v < 4; v++) {
@@ -377,7 +395,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     __syncthreads();
 
     // ---- per segment: fixed-order sum of the waves; finish here, or via the slots
-    auto finish = [&](int k, float v0, float v1) {
+    auto finish = [&](int k, int r, float v0, float v1) {
         const int S = S_first + k;
         const int s = g1_shard_of_seg<ONE>(a, sht, S);
         const int cg = S - sh(s).sbeg;
@@ -387,7 +405,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         v1 *= g1_hi(sv);
         const uint32_t out = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) |
                              ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
-        reinterpret_cast<uint32_t*>(sh(s).C + cg * 128)[lane] = out;
+        reinterpret_cast<uint32_t*>(sh(s).C + r * sh(s).ldc + cg * 128)[lane] = out;
     };
     auto contributors = [&](int k, int& g_lo, int& g_hi) {
         const int S = S_first + k;
@@ -396,23 +414,32 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         g_lo = g1_wg_of(a, segU0);
         g_hi = g1_wg_of(a, segU0 + ntr - 1);
     };
+    const int nr = R == 1 ? 1 : a.nrows;
     bool any_last = false;
     for (int k = wave; k < nseg; k += G1_NW) {
-        float v0 = 0.f, v1 = 0.f;
+        float v0[R], v1[R];
 #pragma unroll
-        for (int ww = 0; ww < G1_NW; ww++) {
-            const float2 p = *reinterpret_cast<const float2*>(red + (k * G1_NW + ww) * 128 + 2 * lane);
-            v0 += p.x;
-            v1 += p.y;
+        for (int r = 0; r < R; r++) {
+            v0[r] = v1[r] = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < G1_NW; ww++) {
+                const float2 p = *reinterpret_cast<const float2*>(red + ((k * G1_NW + ww) * R + r) * 128 + 2 * lane);
+                v0[r] += p.x;
+                v1[r] += p.y;
+            }
         }
         int g_lo, g_hi;
         contributors(k, g_lo, g_hi);
         int is_last = 0;
         if (g_hi > g_lo) {
-            uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + (long)(S_first + k + g) * 128) + lane;
-            const uint64_t pv = (uint64_t)__builtin_bit_cast(uint32_t, v0) |
-                                ((uint64_t)__builtin_bit_cast(uint32_t, v1) << 32);
-            __hip_atomic_store(my, pv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // slot (S + g) holds R rows of 128 partials
+            uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + (long)(S_first + k + g) * R * 128) + lane;
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                const uint64_t pv = (uint64_t)__builtin_bit_cast(uint32_t, v0[r]) |
+                                    ((uint64_t)__builtin_bit_cast(uint32_t, v1[r]) << 32);
+                __hip_atomic_store(my + r * 64, pv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             __builtin_amdgcn_s_waitcnt(0);   // this wave's slot stores are complete
             uint32_t old = 0;
             if (lane == 0)
@@ -425,7 +452,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
             if (is_last && lane == 0)
                 __hip_atomic_store(a.counters + S_first + k, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         } else {
-            finish(k, v0, v1);
+            for (int r = 0; r < nr; r++) finish(k, r, v0[r], v1[r]);
         }
         if (lane == 0) last[k] = is_last;
         any_last |= is_last != 0;
@@ -438,52 +465,58 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
             int g_lo, g_hi;
             contributors(k, g_lo, g_hi);
             const int nsl = g_hi - g_lo + 1;
-            const uint64_t* sl = reinterpret_cast<const uint64_t*>(a.slots + (long)(S_first + k + g_lo) * 128) + lane;
-            float v0 = 0.f, v1 = 0.f;
-            for (int t0 = wave; t0 < nsl; t0 += 8 * G1_NW) {
-                uint64_t xv[8];
+            const uint64_t* sl = reinterpret_cast<const uint64_t*>(a.slots + (long)(S_first + k + g_lo) * R * 128) + lane;
 #pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    const int gg = min(t0 + t * G1_NW, nsl - 1);
-                    xv[t] = __hip_atomic_load(sl + (long)gg * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
+            for (int r = 0; r < R; r++) {
+                float v0 = 0.f, v1 = 0.f;
+                for (int t0 = wave; t0 < nsl; t0 += 8 * G1_NW) {
+                    uint64_t xv[8];
 #pragma unroll
-                for (int t = 0; t < 8; t++) {
-                    if (t0 + t * G1_NW < nsl) {
-                        v0 += __builtin_bit_cast(float, (uint32_t)xv[t]);
-                        v1 += __builtin_bit_cast(float, (uint32_t)(xv[t] >> 32));
+                    for (int t = 0; t < 8; t++) {
+                        const int gg = min(t0 + t * G1_NW, nsl - 1);
+                        xv[t] = __hip_atomic_load(sl + ((long)gg * R + r) * 64, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+                    }
+#pragma unroll
+                    for (int t = 0; t < 8; t++) {
+                        if (t0 + t * G1_NW < nsl) {
+                            v0 += __builtin_bit_cast(float, (uint32_t)xv[t]);
+                            v1 += __builtin_bit_cast(float, (uint32_t)(xv[t] >> 32));
+                        }
                     }
                 }
+                *reinterpret_cast<float2*>(red + ((k * G1_NW + wave) * R + r) * 128 + 2 * lane) = float2{v0, v1};
             }
-            *reinterpret_cast<float2*>(red + (k * G1_NW + wave) * 128 + 2 * lane) = float2{v0, v1};
         }
         __syncthreads();
         for (int k = wave; k < nseg; k += G1_NW) {
             if (!last[k]) continue;
-            float v0 = 0.f, v1 = 0.f;
+            for (int r = 0; r < nr; r++) {
+                float v0 = 0.f, v1 = 0.f;
 #pragma unroll
-            for (int ww = 0; ww < G1_NW; ww++) {
-                const float2 p = *reinterpret_cast<const float2*>(red + (k * G1_NW + ww) * 128 + 2 * lane);
-                v0 += p.x;
-                v1 += p.y;
+                for (int ww = 0; ww < G1_NW; ww++) {
+                    const float2 p = *reinterpret_cast<const float2*>(red + ((k * G1_NW + ww) * R + r) * 128 + 2 * lane);
+                    v0 += p.x;
+                    v1 += p.y;
+                }
+                finish(k, r, v0, v1);
             }
-            finish(k, v0, v1);
         }
     }
 }
 
 // Eight waves per SIMD need at most 64 VGPRs (measured on MI355X: 68 VGPRs leave room for
 // only 6); the SGPR cap keeps the count well inside what eight waves per SIMD may hold.
-template <int K, int CB, bool ONE>
+template <int K, int CB, bool ONE, int R>
 __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8), amdgpu_num_sgpr(74))) void gemv1_kernel(const G1Args a)
 {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-    g1_body<K, CB, ONE>(a.grp, a.sh, blockIdx.x, lds);
+    g1_body<K, CB, ONE, R>(a.grp, a.sh, blockIdx.x, lds);
 }
 
 // Several groups (different K) in one launch: their start-up and reduction tails overlap
 // instead of following each other.
-template <int CB>
+template <int CB, int R>
 __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8), amdgpu_num_sgpr(74))) void gemv1_multi_kernel(const G1Multi)
 {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
@@ -500,29 +533,30 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     const G1Shard* sht = mm.sh + mm.sh0[i];
     const int g = blockIdx.x - mm.gbeg[i];
     switch (mm.K[i]) {
-    case 1: g1_body<1, CB, false>(a, sht, g, lds); break;
-    case 2: g1_body<2, CB, false>(a, sht, g, lds); break;
-    case 3: g1_body<3, CB, false>(a, sht, g, lds); break;
-    case 4: g1_body<4, CB, false>(a, sht, g, lds); break;
-    case 5: g1_body<5, CB, false>(a, sht, g, lds); break;
-    case 6: g1_body<6, CB, false>(a, sht, g, lds); break;
-    case 7: g1_body<7, CB, false>(a, sht, g, lds); break;
-    case 8: g1_body<8, CB, false>(a, sht, g, lds); break;
+    case 1: g1_body<1, CB, false, R>(a, sht, g, lds); break;
+    case 2: g1_body<2, CB, false, R>(a, sht, g, lds); break;
+    case 3: g1_body<3, CB, false, R>(a, sht, g, lds); break;
+    case 4: g1_body<4, CB, false, R>(a, sht, g, lds); break;
+    case 5: g1_body<5, CB, false, R>(a, sht, g, lds); break;
+    case 6: g1_body<6, CB, false, R>(a, sht, g, lds); break;
+    case 7: g1_body<7, CB, false, R>(a, sht, g, lds); break;
+    case 8: g1_body<8, CB, false, R>(a, sht, g, lds); break;
     }
 }
 
 // ---------------------------------------------------------------- host side
 
-template <int K, int CB>
+template <int K, int CB, int R>
 static const void* g1_fn(bool one)
 {
-    return one ? reinterpret_cast<const void*>(&gemv1_kernel<K, CB, true>)
-               : reinterpret_cast<const void*>(&gemv1_kernel<K, CB, false>);
+    return one ? reinterpret_cast<const void*>(&gemv1_kernel<K, CB, true, R>)
+               : reinterpret_cast<const void*>(&gemv1_kernel<K, CB, false, R>);
 }
 
+template <int R>
 static const void* g1_fn_kcb(int K, int cb, bool one)
 {
-#define EXL3_CASE(KK) case KK: return cb == CB_MCG ? g1_fn<KK, CB_MCG>(one) : g1_fn<KK, CB_3INST>(one);
+#define EXL3_CASE(KK) case KK: return cb == CB_MCG ? g1_fn<KK, CB_MCG, R>(one) : g1_fn<KK, CB_3INST, R>(one);
     switch (K) {
         EXL3_CASE(1) EXL3_CASE(2) EXL3_CASE(3) EXL3_CASE(4)
         EXL3_CASE(5) EXL3_CASE(6) EXL3_CASE(7) EXL3_CASE(8)
@@ -558,20 +592,24 @@ static G1Div g1_magic(uint32_t d)
 // activation block for each 128-input block it can meet (at most ceil(L / 8) + nseg + 1:
 // a piece of a segment meets one block more than its length in blocks when it starts
 // inside a block, and only the first piece can).
-static size_t g1_lds_bytes(int U, int G, int ntr)
+static size_t g1_lds_bytes(int U, int G, int ntr, int R)
 {
     const int L = (U + G - 1) / G;
     const int nseg = (L - 1 + ntr - 1) / ntr + 1;
     const int nocc = (L + 7) / 8 + nseg + 1;
-    return (size_t)nseg * (G1_NW * 128 * sizeof(float) + 4) + (size_t)nocc * 128 * sizeof(uint32_t);
+    return (size_t)nseg * (G1_NW * R * 128 * sizeof(float) + 4) + (size_t)nocc * R * 128 * sizeof(uint32_t);
 }
 
-// Per-shard share of the workspace after the counter area: slot rows for up to G1_GMAX
-// workgroups and one per column group.
-size_t gemv1_slot_bytes(int ic, int oc)
+// Row-count template of a call: one activation row, or up to four (G1_ROWS).
+constexpr int G1_ROWS = 4;
+static int g1_R(int rows) { return rows == 1 ? 1 : G1_ROWS; }
+
+// Per-shard share of the workspace after the counter area: slots of R rows for up to
+// G1_GMAX workgroups and one per column group.
+size_t gemv1_slot_bytes(int ic, int oc, int rows)
 {
     (void)ic;
-    return (size_t)(G1_GMAX + oc / 128) * 128 * sizeof(float);
+    return (size_t)(G1_GMAX + oc / 128) * g1_R(rows) * 128 * sizeof(float);
 }
 
 // Units per workgroup the launch aims for: fewer, longer ranges cut the cross-workgroup
@@ -583,10 +621,11 @@ constexpr int G1_UNITS_PER_WG = 32;
 // Fills one group from shards[idx[0..n-1]] (same K and codebook) into table entries
 // tab[0..n-1]; returns its unit count.
 static long g1_group(G1Group& grp, G1Shard* tab, const GemvShard* shards, const int* idx, int n, const uint16_t* A,
-                     int ntr)
+                     int ntr, int rows)
 {
     grp = G1Group{};
     grp.x = A;
+    grp.nrows = rows;
     grp.ntr = ntr;
     grp.nshards = n;
     long U = 0;
@@ -598,6 +637,7 @@ static long g1_group(G1Group& grp, G1Shard* tab, const GemvShard* shards, const 
         e.suh = d.suh;
         e.svh = d.svh;
         e.C = d.C;
+        e.ldc = d.ldc;
         e.ubeg = (int)U;
         e.sbeg = nsegs;
         e.oc16 = d.oc / 16;
@@ -610,7 +650,7 @@ static long g1_group(G1Group& grp, G1Shard* tab, const GemvShard* shards, const 
 }
 
 // Workgroup split of a group of U units into G ranges, and its share of counters and slots.
-static int g1_place(G1Group& grp, long U, int G, uint32_t* counters, int& cbase, int max_counters, char* slots,
+static int g1_place(G1Group& grp, long U, int G, int R, uint32_t* counters, int& cbase, int max_counters, char* slots,
                     size_t& sbase, size_t slot_bytes)
 {
     if (U > (1L << 30))
@@ -618,7 +658,7 @@ static int g1_place(G1Group& grp, long U, int G, uint32_t* counters, int& cbase,
     if (cbase + grp.nsegs > max_counters)
         return set_error(EXL3_ERR_ARG, "exl3_gemv: %d column groups exceed the %d segment counters",
                          cbase + grp.nsegs, max_counters);
-    const size_t need = (size_t)(G + grp.nsegs) * 128 * sizeof(float);
+    const size_t need = (size_t)(G + grp.nsegs) * R * 128 * sizeof(float);
     if (sbase + need > slot_bytes)
         return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: slot area of %zu bytes, %zu needed", slot_bytes,
                          sbase + need);
@@ -645,20 +685,70 @@ static int g1_launch(const void* fn, void* arg, int G, size_t lds, hipStream_t s
     }
     void* kargs[] = {arg};
     hipLaunchKernel(fn, dim3(G), dim3(64 * G1_NW), kargs, lds, stream);
-    return check_launch("exl3_gemv (batch 1)");
+    return check_launch("exl3_gemv (1-4 rows)");
 }
 
-// Batch 1: the shards are grouped by (K, codebook), at most G1_MAXSH shards a group.  A
-// launch takes whole groups of one codebook, at most G1_MAXSH shards in all: one group is
-// a gemv1_kernel launch, several share a gemv1_multi_kernel launch with their workgroup
-// counts scaled to the resident limit together.
-int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint32_t* counters, int max_counters,
-                   char* slots, size_t slot_bytes, hipStream_t stream)
+// Workgroup counts G[0..ns) of one launch whose groups have U[t] units, for the most
+// workgroups per CU (up to G1_WG_PER_CU) whose LDS lets them all stay resident; returns
+// that number and the launch's LDS per workgroup.
+static int g1_split(const long* U, int ns, int ntr, int R, int cus, int* G, size_t& lds)
 {
+    constexpr size_t LDS_PER_CU = 160 * 1024;
+    int wgpc = G1_WG_PER_CU;
+    for (; wgpc >= 1; wgpc--) {
+        const int gmax = std::min(G1_GMAX, wgpc * cus);
+        long Gsum = 0;
+        for (int t = 0; t < ns; t++) {
+            G[t] = (int)std::min<long>(gmax, std::max<long>(1, U[t] / G1_UNITS_PER_WG));
+            Gsum += G[t];
+        }
+        if (Gsum > gmax)   // share the resident workgroups in proportion to the groups' sizes
+            for (int t = 0; t < ns; t++) G[t] = std::max(1, (int)((long)G[t] * gmax / Gsum));
+        lds = 0;
+        for (int t = 0; t < ns; t++) lds = std::max(lds, g1_lds_bytes((int)U[t], G[t], ntr, R));
+        if ((size_t)wgpc * lds <= LDS_PER_CU) break;
+    }
+    return std::max(wgpc, 1);
+}
+
+// Whether 2..4 rows of these shards run well here: every launch keeps at least three
+// workgroups per CU resident (with four rows the LDS per workgroup grows with its range).
+// The caller takes the split kernels otherwise.
+bool gemv1_rows_fit(const GemvShard* shards, int nshards)
+{
+    const int ntr = shards[0].ic / 16;
+    const int cus = g1_cu_count();
+    // the launches group shards of one codebook; bound each launch by all of its shards
+    for (int cb = 0; cb < 2; cb++) {
+        long U[G1_MAXSH];
+        int ns = 0, G[G1_MAXSH];
+        for (int i = 0; i < nshards; i++) {
+            if (shards[i].cb != cb) continue;
+            const long u = (long)(shards[i].oc / 128) * ntr;
+            if (ns < G1_MAXSH) U[ns++] = u;
+            else U[G1_MAXSH - 1] += u;
+        }
+        if (!ns) continue;
+        size_t lds;
+        if (g1_split(U, ns, ntr, G1_ROWS, cus, G, lds) < 3) return false;
+    }
+    return true;
+}
+
+// 1..4 activation rows: the shards are grouped by (K, codebook), at most G1_MAXSH shards a
+// group.  A launch takes whole groups of one codebook, at most G1_MAXSH shards in all: one
+// group is a gemv1_kernel launch, several share a gemv1_multi_kernel launch with their
+// workgroup counts scaled to the resident limit together.  Workgroups per CU: four, or
+// fewer where a launch's LDS per workgroup (larger with four rows) would not let four
+// stay resident.
+int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, uint32_t* counters,
+                   int max_counters, char* slots, size_t slot_bytes, hipStream_t stream)
+{
+    if (rows < 1 || rows > G1_ROWS) return set_error(EXL3_ERR_ARG, "exl3_gemv: rows=%d is not in 1..%d", rows, G1_ROWS);
+    const int R = g1_R(rows);
     const int ic = shards[0].ic;
     const int ntr = ic / 16;
-    const int gmax = std::min(G1_GMAX, G1_WG_PER_CU * g1_cu_count());
-    auto g_of = [&](long U) { return (int)std::min<long>(gmax, std::max<long>(1, U / G1_UNITS_PER_WG)); };
+    const int cus = g1_cu_count();
 
     // groups: shard indices by (codebook, K) in first-seen order, split every G1_MAXSH shards
     constexpr int MAXG = EXL3_MAX_SHARDS;
@@ -690,42 +780,42 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, uint
                 done[j] = true;
             }
         const int cb = gcb[j0];
-        if (ns == 1) {
-            G1Args args = {};
-            const long U = g1_group(args.grp, args.sh, shards, gidx[j0], gn[j0], A, ntr);
-            const int G = g_of(U);
-            int rc = g1_place(args.grp, U, G, counters, cbase, max_counters, slots, sbase, slot_bytes);
-            if (rc != EXL3_OK) return rc;
-            rc = g1_launch(g1_fn_kcb(gK[j0], cb, gn[j0] == 1), &args, G, g1_lds_bytes((int)U, G, ntr), stream);
-            if (rc != EXL3_OK) return rc;
-            continue;
-        }
         G1Multi m = {};
-        long U[G1_MAXSH], Gsum = 0;
+        long U[G1_MAXSH];
         int G[G1_MAXSH], sh0 = 0;
         for (int t = 0; t < ns; t++) {
             const int j = sel[t];
             m.sh0[t] = sh0;
             m.K[t] = gK[j];
-            U[t] = g1_group(m.grp[t], m.sh + sh0, shards, gidx[j], gn[j], A, ntr);
+            U[t] = g1_group(m.grp[t], m.sh + sh0, shards, gidx[j], gn[j], A, ntr, rows);
             sh0 += gn[j];
-            G[t] = g_of(U[t]);
-            Gsum += G[t];
         }
-        if (Gsum > gmax)   // share the resident workgroups in proportion to the groups' sizes
-            for (int t = 0; t < ns; t++) G[t] = std::max(1, (int)((long)G[t] * gmax / Gsum));
         size_t lds = 0;
+        g1_split(U, ns, ntr, R, cus, G, lds);
+        if (ns == 1) {
+            G1Args args = {};
+            args.grp = m.grp[0];
+            for (int i = 0; i < gn[sel[0]]; i++) args.sh[i] = m.sh[i];
+            int rc = g1_place(args.grp, U[0], G[0], R, counters, cbase, max_counters, slots, sbase, slot_bytes);
+            if (rc != EXL3_OK) return rc;
+            const bool one = gn[sel[0]] == 1;
+            const void* fn = R == 1 ? g1_fn_kcb<1>(gK[sel[0]], cb, one) : g1_fn_kcb<G1_ROWS>(gK[sel[0]], cb, one);
+            rc = g1_launch(fn, &args, G[0], lds, stream);
+            if (rc != EXL3_OK) return rc;
+            continue;
+        }
         int gb = 0;
         for (int t = 0; t < ns; t++) {
-            const int rc = g1_place(m.grp[t], U[t], G[t], counters, cbase, max_counters, slots, sbase, slot_bytes);
+            const int rc = g1_place(m.grp[t], U[t], G[t], R, counters, cbase, max_counters, slots, sbase, slot_bytes);
             if (rc != EXL3_OK) return rc;
             m.gbeg[t] = gb;
             gb += G[t];
-            lds = std::max(lds, g1_lds_bytes((int)U[t], G[t], ntr));
         }
         m.ngrp = ns;
-        const void* fn = cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG>)
-                                      : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST>);
+        const void* fn = R == 1 ? (cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG, 1>)
+                                               : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST, 1>))
+                                : (cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG, G1_ROWS>)
+                                               : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST, G1_ROWS>));
         const int rc = g1_launch(fn, &m, gb, lds, stream);
         if (rc != EXL3_OK) return rc;
     }
