@@ -64,6 +64,7 @@ struct SkShard {
     uint16_t* C;               // (rows, ldc) fp16, columns [0, oc)
     long ldc;
     int oc, ntn, tbeg;         // outputs, 256-wide tile columns, first tile of the shard
+    int K;                     // bits per weight (read by the per-shard-K kernel)
 };
 
 struct SkArgs {
@@ -197,6 +198,8 @@ __device__ __forceinline__ void sk_load(uint32_t (&w)[K + 1], const uint32_t* __
     }
 }
 
+// K > 0: every shard of the launch has K bits per weight; K = 0: each tile piece takes its
+// shard's K (one launch for shards of different bit widths).
 template <int K, int CB, int BM>
 __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(BM == 256 ? 2 : 6, BM == 256 ? 2 : 6)))
 void gemm_sk_kernel(const SkArgs a)
@@ -227,7 +230,6 @@ void gemm_sk_kernel(const SkArgs a)
 
     f32x4 acc[MB][NB];
     uint4 areg[AP];
-    uint32_t w[K + 1];
 
     const long u_begin = sk_first(a, g), u_end = sk_first(a, g + 1);
     long u = u_begin;
@@ -247,93 +249,112 @@ void gemm_sk_kernel(const SkArgs a)
         const int btn = 16 * tn + (btile & 15);
         const bool bok = btn < tc;
 
-        auto load_step = [&](int s) {
-#pragma unroll
-            for (int p = 0; p < AP; p++) {
-                const int row = m0 + 64 * p + arow;
-                areg[p] = (aload && row < a.rows)
-                    ? *reinterpret_cast<const uint4*>(S.Ah + (long)row * a.ic + s * SK_KS + aseg * 8)
-                    : uint4{0u, 0u, 0u, 0u};
-            }
-            const int ti = 4 * s + (btile >> 4);
-            sk_load<K>(w, S.trellis + ((long)ti * tc + (bok ? btn : 0)) * (8 * K) + c * K, bok);
-        };
-        // the registers of a K-step into LDS buffer b: A as loaded, B decoded
-        auto store_step = [&](int b) {
-            _Float16* as = As(b);
-            _Float16* bs = Bs(b);
-#pragma unroll
-            for (int p = 0; p < AP; p++)
-                if (aload) *reinterpret_cast<uint4*>(as + (64 * p + arow) * SK_LD + aseg * 8) = areg[p];
-            chunk_prev_dpp<K>(w, first_lane);
-            uint4 o[4];
-            sk_decode<K, CB>(w, kc, o);
-            *reinterpret_cast<uint4*>(bs + bn0 * SK_LD + bk0) = o[0];
-            *reinterpret_cast<uint4*>(bs + bn0 * SK_LD + bk0 + 8) = o[1];
-            *reinterpret_cast<uint4*>(bs + (bn0 + 8) * SK_LD + bk0) = o[2];
-            *reinterpret_cast<uint4*>(bs + (bn0 + 8) * SK_LD + bk0 + 8) = o[3];
-        };
-        // the MFMAs of one K-step from LDS buffer b
-        auto mfma_step = [&](int b) {
-            const _Float16* as = As(b);
-            const _Float16* bs = Bs(b);
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                f16x8 bf[NB];
-#pragma unroll
-                for (int nb = 0; nb < NB; nb++)
-                    bf[nb] = *reinterpret_cast<const f16x8*>(bs + (NB * 16 * wn + 16 * nb + (lane & 15)) * SK_LD +
-                                                             32 * h + 8 * (lane >> 4));
-#pragma unroll
-                for (int mb = 0; mb < MB; mb++) {
-                    const f16x8 af = *reinterpret_cast<const f16x8*>(as + (MB * 16 * wm + 16 * mb + (lane & 15)) * SK_LD +
-                                                                     32 * h + 8 * (lane >> 4));
-#pragma unroll
-                    for (int nb = 0; nb < NB; nb++) acc[mb][nb] = mfma16x16x32(af, bf[nb], acc[mb][nb]);
-                }
-            }
-        };
-
 #pragma unroll
         for (int mb = 0; mb < MB; mb++)
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // the piece's K-steps, for KK bits per weight
+        auto run_piece = [&](auto kk) {
+            constexpr int KK = decltype(kk)::value;
+            uint32_t w[KK + 1];
+            auto load_step = [&](int s) {
+#pragma unroll
+                for (int p = 0; p < AP; p++) {
+                    const int row = m0 + 64 * p + arow;
+                    areg[p] = (aload && row < a.rows)
+                        ? *reinterpret_cast<const uint4*>(S.Ah + (long)row * a.ic + s * SK_KS + aseg * 8)
+                        : uint4{0u, 0u, 0u, 0u};
+                }
+                const int ti = 4 * s + (btile >> 4);
+                sk_load<KK>(w, S.trellis + ((long)ti * tc + (bok ? btn : 0)) * (8 * KK) + c * KK, bok);
+            };
+            // the registers of a K-step into LDS buffer b: A as loaded, B decoded
+            auto store_step = [&](int b) {
+                _Float16* as = As(b);
+                _Float16* bs = Bs(b);
+#pragma unroll
+                for (int p = 0; p < AP; p++)
+                    if (aload) *reinterpret_cast<uint4*>(as + (64 * p + arow) * SK_LD + aseg * 8) = areg[p];
+                chunk_prev_dpp<KK>(w, first_lane);
+                uint4 o[4];
+                sk_decode<KK, CB>(w, kc, o);
+                *reinterpret_cast<uint4*>(bs + bn0 * SK_LD + bk0) = o[0];
+                *reinterpret_cast<uint4*>(bs + bn0 * SK_LD + bk0 + 8) = o[1];
+                *reinterpret_cast<uint4*>(bs + (bn0 + 8) * SK_LD + bk0) = o[2];
+                *reinterpret_cast<uint4*>(bs + (bn0 + 8) * SK_LD + bk0 + 8) = o[3];
+            };
+            // the MFMAs of one K-step from LDS buffer b
+            auto mfma_step = [&](int b) {
+                const _Float16* as = As(b);
+                const _Float16* bs = Bs(b);
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    f16x8 bf[NB];
+#pragma unroll
+                    for (int nb = 0; nb < NB; nb++)
+                        bf[nb] = *reinterpret_cast<const f16x8*>(bs + (NB * 16 * wn + 16 * nb + (lane & 15)) * SK_LD +
+                                                                 32 * h + 8 * (lane >> 4));
+#pragma unroll
+                    for (int mb = 0; mb < MB; mb++) {
+                        const f16x8 af = *reinterpret_cast<const f16x8*>(as + (MB * 16 * wm + 16 * mb + (lane & 15)) * SK_LD +
+                                                                         32 * h + 8 * (lane >> 4));
+#pragma unroll
+                        for (int nb = 0; nb < NB; nb++) acc[mb][nb] = mfma16x16x32(af, bf[nb], acc[mb][nb]);
+                    }
+                }
+            };
 
-        load_step(s0);
-        if constexpr (sk_nbuf<BM>() == 2) {
-            // Software pipeline over two LDS buffers, one barrier per K-step: during step s the
-            // MFMAs read buffer (s - s0) % 2 while the step s + 1 tiles (loaded into registers
-            // a step earlier) are decoded into the other buffer and step s + 2 is loaded.  The
-            // step is one basic block (the last steps re-decode and re-load in-bounds data that
-            // is never read), so the scheduler can issue the decode's VALU work between the
-            // MFMAs, which run on the matrix pipe meanwhile.
-            store_step(0);
-            load_step(min(s0 + 1, s1 - 1));
-            __syncthreads();
-            if (wave < SK_WAVES / 2) {
-                for (int s = s0; s < s1; s++) {
-                    const int b = (s - s0) & 1;
-                    mfma_step(b);
-                    store_step(b ^ 1);
-                    load_step(min(s + 2, s1 - 1));
-                    __syncthreads();          // buffer b ^ 1 is complete; buffer b is free
+
+            load_step(s0);
+            if constexpr (sk_nbuf<BM>() == 2) {
+                // Software pipeline over two LDS buffers, one barrier per K-step: during step s the
+                // MFMAs read buffer (s - s0) % 2 while the step s + 1 tiles (loaded into registers
+                // a step earlier) are decoded into the other buffer and step s + 2 is loaded.  The
+                // step is one basic block (the last steps re-decode and re-load in-bounds data that
+                // is never read), so the scheduler can issue the decode's VALU work between the
+                // MFMAs, which run on the matrix pipe meanwhile.
+                store_step(0);
+                load_step(min(s0 + 1, s1 - 1));
+                __syncthreads();
+                if (wave < SK_WAVES / 2) {
+                    for (int s = s0; s < s1; s++) {
+                        const int b = (s - s0) & 1;
+                        mfma_step(b);
+                        store_step(b ^ 1);
+                        load_step(min(s + 2, s1 - 1));
+                        __syncthreads();          // buffer b ^ 1 is complete; buffer b is free
+                    }
+                } else {
+                    for (int s = s0; s < s1; s++) {
+                        const int b = (s - s0) & 1;
+                        store_step(b ^ 1);
+                        load_step(min(s + 2, s1 - 1));
+                        mfma_step(b);
+                        __syncthreads();          // buffer b ^ 1 is complete; buffer b is free
+                    }
                 }
             } else {
                 for (int s = s0; s < s1; s++) {
-                    const int b = (s - s0) & 1;
-                    store_step(b ^ 1);
-                    load_step(min(s + 2, s1 - 1));
-                    mfma_step(b);
-                    __syncthreads();          // buffer b ^ 1 is complete; buffer b is free
+                    __syncthreads();              // the previous step's MFMAs are done with LDS
+                    store_step(0);
+                    __syncthreads();
+                    if (s + 1 < s1) load_step(s + 1);
+                    mfma_step(0);
                 }
             }
+        };
+        if constexpr (K > 0) {
+            run_piece(std::integral_constant<int, K>{});
         } else {
-            for (int s = s0; s < s1; s++) {
-                __syncthreads();              // the previous step's MFMAs are done with LDS
-                store_step(0);
-                __syncthreads();
-                if (s + 1 < s1) load_step(s + 1);
-                mfma_step(0);
+            switch (S.K) {
+            case 1: run_piece(std::integral_constant<int, 1>{}); break;
+            case 2: run_piece(std::integral_constant<int, 2>{}); break;
+            case 3: run_piece(std::integral_constant<int, 3>{}); break;
+            case 4: run_piece(std::integral_constant<int, 4>{}); break;
+            case 5: run_piece(std::integral_constant<int, 5>{}); break;
+            case 6: run_piece(std::integral_constant<int, 6>{}); break;
+            case 7: run_piece(std::integral_constant<int, 7>{}); break;
+            default: run_piece(std::integral_constant<int, 8>{}); break;
             }
         }
         u += s1 - s0;
@@ -486,6 +507,8 @@ template <int BM>
 static const void* sk_fn_kcb(int K, int cb)
 {
 #define EXL3_CASE(KK) case KK: return cb == CB_MCG ? sk_fn<KK, CB_MCG, BM>() : sk_fn<KK, CB_3INST, BM>();
+    if constexpr (BM == 16)
+        if (K == 0) return cb == CB_MCG ? sk_fn<0, CB_MCG, 16>() : sk_fn<0, CB_3INST, 16>();   // per-shard K
     switch (K) {
         EXL3_CASE(1) EXL3_CASE(2) EXL3_CASE(3) EXL3_CASE(4)
         EXL3_CASE(5) EXL3_CASE(6) EXL3_CASE(7) EXL3_CASE(8)
@@ -519,7 +542,7 @@ static int sk_launch(SkArgs& a, int K, int cb, char* ws, size_t ws_bytes, const 
         if (rc != EXL3_OK) return rc;
     }
     const void* fn = sk_fn_kcb<BM>(K, cb);
-    if (!fn) return set_error(EXL3_ERR_ARG, "%s: K=%d is not in 1..8", what, K);
+    if (!fn) return set_error(EXL3_ERR_ARG, "%s: K=%d is not in 1..8", what, K);   // K = 0: per shard
     if (sk_lds<BM>() > 64 * 1024) {
         hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, sk_lds<BM>());
         (void)hipGetLastError();
@@ -547,12 +570,14 @@ int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, c
     s.oc = oc;
     s.ntn = sk_ntn(oc);
     s.tbeg = 0;
+    s.K = K;
     a.ntiles = ((rows + 255) / 256) * s.ntn;
     return sk_launch<256>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
 }
 
-// 2..16 rows: per (K, codebook) group of up to SK_MAXSH shards, one set-up kernel (the
-// shards' activations, the group's tile counters) and one stream-K launch with 16-row tiles.
+// 2..16 rows: per codebook, groups of up to SK_MAXSH shards; per group one set-up kernel
+// (the shards' activations, the group's tile counters) and one stream-K launch with 16-row
+// tiles -- a single-K kernel when the group's shards share K, else the per-shard-K one.
 int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws, size_t ws_bytes,
                      hipStream_t stream)
 {
@@ -569,10 +594,11 @@ int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, in
         a.nks = ic / SK_KS;
         p.A = A;
         p.nblk = ic / 128;
-        int tiles = 0;
+        int tiles = 0, K = shards[i].K;
         for (int s = i; s < nshards && a.nshards < SK_MAXSH; s++) {
-            if (done[s] || shards[s].K != shards[i].K || shards[s].cb != shards[i].cb) continue;
+            if (done[s] || shards[s].cb != shards[i].cb) continue;
             const GemvShard& d = shards[s];
+            if (d.K < 1 || d.K > 8) return set_error(EXL3_ERR_ARG, "exl3_gemv: K=%d is not in 1..8", d.K);
             if (off + ah > ws_bytes)
                 return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: workspace of %zu bytes is too small", ws_bytes);
             uint16_t* Ah = reinterpret_cast<uint16_t*>(ws + off);
@@ -588,6 +614,8 @@ int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, in
             e.oc = d.oc;
             e.ntn = sk_ntn(d.oc);
             e.tbeg = tiles;
+            e.K = d.K;
+            if (d.K != K) K = 0;
             tiles += e.ntn;
             done[s] = true;
         }
@@ -600,7 +628,7 @@ int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, in
         if (rc != EXL3_OK) return rc;
         const size_t need = sk_ws<16>(tiles, sk_gmax<16>());
         const size_t avail = ws_bytes > off ? ws_bytes - off : 0;
-        rc = sk_launch<16>(a, shards[i].K, shards[i].cb, ws + off, std::min(need, avail), "exl3_gemv", stream, false);
+        rc = sk_launch<16>(a, K, shards[i].cb, ws + off, std::min(need, avail), "exl3_gemv", stream, false);
         if (rc != EXL3_OK) return rc;
         off += std::min(need, avail);
     }
