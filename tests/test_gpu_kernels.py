@@ -116,7 +116,8 @@ def check_linear_out(y, x, lin, cb, oracle, W=None):
 @pytest.mark.parametrize("K", range(1, 9))
 @pytest.mark.parametrize("rows", [1, 4, 5, 16])
 def test_gemv_small_all_K(native, oracle, K, rows):
-    """1 row: the persistent kernel; 2..4: the split kernels; 5..16: 16-row stream-K tiles"""
+    """1..4 rows: the persistent kernel (4 rows in the MFMA's A operand); 5..16: 16-row
+    stream-K tiles"""
     lin = syn.linear(512, 384, K, seed=100 + K)
     x = syn.activations(rows, 512, torch.Generator().manual_seed(rows))
     d = to_gpu(lin)
@@ -150,9 +151,12 @@ def test_gemv_deterministic_and_workspace_rearmed(native):
         assert torch.equal(y, ys[0])
 
 
-@pytest.mark.parametrize("rows", [1, 4, 16])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 9, 16])
 def test_gemv_grouped_config2(native, oracle, rows):
-    """qkv: q K4 5120->6144, k/v K5 5120->1024; gate_up: 2 x K3 5120->17408."""
+    """qkv: q K4 5120->6144, k/v K5 5120->1024; gate_up: 2 x K3 5120->17408.  Rows 2..4 take
+    the 1..4-row kernel for qkv and the split kernels for gate_up (its 17408-wide launch
+    would not keep three workgroups per CU resident); 9 and 16 rows the 16-row tiles, qkv's
+    mixed K in one launch."""
     x = syn.activations(rows, 5120, torch.Generator().manual_seed(20 + rows))
     for spec in ([(6144, 4), (1024, 5), (1024, 5)], [(17408, 3), (17408, 3)]):
         lins = [syn.linear(5120, oc, K, seed=200 + i) for i, (oc, K) in enumerate(spec)]
@@ -166,10 +170,11 @@ def test_gemv_grouped_config2(native, oracle, rows):
 
 @pytest.mark.parametrize("ic,ocs,K", [(128, [131200], 2), (256, [384, 128, 640], 3), (384, [1152], 5),
                                       (2048, [128], 4), (256, [2048, 2048], 4), (640, [128, 256, 128], 6)])
-def test_gemv1_workgroup_ranges(native, oracle, ic, ocs, K):
-    """Batch 1 with workgroup ranges that span several column groups and shards, start
+@pytest.mark.parametrize("rows", [1, 3])
+def test_gemv1_workgroup_ranges(native, oracle, ic, ocs, K, rows):
+    """1 and 3 rows with workgroup ranges that span several column groups and shards, start
     inside a 128-input block, or cover a whole launch."""
-    x = syn.activations(1, ic, torch.Generator().manual_seed(ic + K))
+    x = syn.activations(rows, ic, torch.Generator().manual_seed(ic + K))
     lins = [syn.linear(ic, oc, K, seed=300 + i) for i, oc in enumerate(ocs)]
     shards = [dict(to_gpu(l), codebook=0) for l in lins]
     y = native.gemv_grouped(x.to(dev()), shards)
