@@ -456,7 +456,7 @@ def main():
                    "hbm_frac": round(r["value"] / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["frac"], 4), "traffic": traffic,
-                     "kernel": f"exl3_gemv K={r['dom']}: gemv1_kernel<{r['dom']}, 0> (one launch per call)",
+                     "kernel": f"exl3_gemv K={r['dom']}: gemv1_kernel<{r['dom']}, 0, true, 1> (one launch per call)",
                      "bytes_per_launch": dom["bytes"], "mean_launch_us": round(dom["mean_us"], 3)},
         "per_K": {str(K): {"GB/s": round(v["gbs"], 1), "frac": round(v["frac"], 4),
                            "mean_us": round(v["mean_us"], 3)} for K, v in r["per_k"].items()},
