@@ -7,9 +7,10 @@ kernels only enqueue on the current stream, so it can be captured in a HIP graph
 
 Dispatch on the number of activation rows (reference: orcasaq2/ops.py:25, 46-59):
   * rows <= 16            fused decode-GEMV (exl3_gemv): packed words streamed from HBM and
-                          decoded in registers, never stored; rows 1: one persistent kernel
-                          (dot products on the VALU, split reduction fused in); rows 2..4: MFMA
-                          partial sums + a reduce kernel; rows 5..16: stream-K over 16-row
+                          decoded in registers, never stored; rows 1..4: one persistent kernel
+                          (MFMA multiply-accumulate, split reduction fused in; rows 2..4 take
+                          MFMA partial sums + a reduce kernel where that kernel's LDS would not
+                          keep enough workgroups resident); rows 5..16: stream-K over 16-row
                           tiles; output Hadamard and svh in the last step;
   * 16 < rows <= GEMM_MAX_ROWS
                           fused decode-GEMM (exl3_gemm): Hadamard pass over x, then tiles

@@ -50,10 +50,15 @@ def test_shard_gemm_wrong_width_message(native):
         torch.ops.orcasaq2.shard_gemm(x, lin["trellis"], lin["suh"], lin["svh"], 256, 3.0, False, False)
 
 
-def test_hip_graph_capture_replays(native, oracle):
+@pytest.mark.parametrize("rows", [1, 2, 9])
+def test_hip_graph_capture_replays(native, oracle, rows):
+    """The op and the grouped op captured into a HIP graph and replayed four times, with
+    eager work between replays, against eager results: 1 row (persistent kernel, its
+    counters rearmed by every call), 2 rows (four-row template), 9 rows (16-row tiles,
+    one launch over both K)."""
     lins = [syn.linear(1024, oc, K, seed=i) for i, (oc, K) in enumerate([(512, 4), (256, 5)])]
     ds = [on(l) for l in lins]
-    x = syn.activations(2, 1024, torch.Generator().manual_seed(1)).to(D)
+    x = syn.activations(rows, 1024, torch.Generator().manual_seed(1)).to(D)
 
     def step():
         a = torch.ops.orcasaq2.shard_gemm(x, ds[0]["trellis"], ds[0]["suh"], ds[0]["svh"], 512, 4.0, False, False)
@@ -72,7 +77,7 @@ def test_hip_graph_capture_replays(native, oracle):
     with torch.cuda.graph(g):
         out = step()
     for i in range(4):
-        x.copy_(syn.activations(2, 1024, torch.Generator().manual_seed(1)).to(D))
+        x.copy_(syn.activations(rows, 1024, torch.Generator().manual_seed(1)).to(D))
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out[0], eager[0]) and torch.equal(out[1], eager[1]), i
