@@ -410,20 +410,43 @@ __device__ __forceinline__ void chunk_prev_dpp(uint32_t (&w)[K + 1], bool first_
 
 // In-wave normalised Walsh-Hadamard of one 128-vector held as v0 = x[2l], v1 = x[2l+1]
 // in lane l (Sylvester order: x'[i] = sum_j (-1)^popcount(i&j) x[j] / sqrt(128)).
+// Butterfly partner: lane ^ d (d <= 16 by ds_swizzle's xor mode within 32-lane halves, no
+// address arithmetic; d = 32 by ds_bpermute).
+template <int D>
+__device__ __forceinline__ float fwht_partner(float v)
+{
+    if constexpr (D < 32)
+        return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1f | (D << 10)));
+    else
+        return __shfl_xor(v, D, 64);
+}
+
+template <int D>
+__device__ __forceinline__ void fwht_round(float& v0, float& v1, int lane)
+{
+    // lower lane: v + partner, upper lane: partner - v -- one fma with a +-1 factor each
+    // (the same single rounding as the add or the subtraction)
+    const float sg = (lane & D) ? -1.f : 1.f;
+    const float p0 = fwht_partner<D>(v0), p1 = fwht_partner<D>(v1);
+    v0 = __builtin_fmaf(sg, v0, p0);
+    v1 = __builtin_fmaf(sg, v1, p1);
+}
+
 __device__ __forceinline__ void wave_fwht128(float& v0, float& v1)
 {
-    const int lane = threadIdx.x & 63;
+    // The empty asm keeps the per-lane signs below from being hoisted out of the caller's
+    // loops (six more live registers across a persistent kernel's main loop).
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
     float a = v0 + v1, b = v0 - v1;
     v0 = a;
     v1 = b;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        float p0 = __shfl_xor(v0, d, 64);
-        float p1 = __shfl_xor(v1, d, 64);
-        const bool upper = (lane & d) != 0;
-        v0 = upper ? (p0 - v0) : (v0 + p0);
-        v1 = upper ? (p1 - v1) : (v1 + p1);
-    }
+    fwht_round<1>(v0, v1, lane);
+    fwht_round<2>(v0, v1, lane);
+    fwht_round<4>(v0, v1, lane);
+    fwht_round<8>(v0, v1, lane);
+    fwht_round<16>(v0, v1, lane);
+    fwht_round<32>(v0, v1, lane);
     const float norm = 0.08838834764831845f;  // 1/sqrt(128)
     v0 *= norm;
     v1 *= norm;
