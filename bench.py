@@ -300,7 +300,7 @@ def config2_bench(reps: int) -> dict:
 
 def config3_bench(reps: int) -> dict:
     """Config 3: prefill GEMM of M=2048 rows through down_proj (17408 -> 5120, K=4), and a
-    standalone reconstruct of the same weight to fp16 (ic, oc)."""
+    standalone reconstruct of the same weight to fp16, as (ic, oc) and as (oc, ic)."""
     import torch
     from orcasaq2 import _native
     from orcasaq2 import synthetic as syn
@@ -312,6 +312,7 @@ def config3_bench(reps: int) -> dict:
     x = torch.randn(M, ic, generator=g, device=dev).half()
     y = torch.empty(M, oc, dtype=torch.half, device=dev)
     W = torch.empty(ic, oc, dtype=torch.half, device=dev)
+    Wt = torch.empty(oc, ic, dtype=torch.half, device=dev)
 
     def gemm():
         _native.gemm(x, lin["trellis"], lin["suh"], lin["svh"], K, 0, out=y)
@@ -319,9 +320,12 @@ def config3_bench(reps: int) -> dict:
     def recon():
         _native.reconstruct(lin["trellis"], K, 0, out=W)
 
+    def recon_t():
+        _native.reconstruct_t(lin["trellis"], K, 0, out=Wt)
+
     def op():
-        # the plugin's path for M > GEMM_MAX_ROWS: had_r_128 -> reconstruct -> library fp16
-        # GEMM -> had_r_128 (orcasaq2/ops.py:50-59 of the reference)
+        # the plugin's path for M > GEMM_MAX_ROWS: had_r_128 -> reconstruct (transposed) ->
+        # library fp16 GEMM -> had_r_128 (orcasaq2/ops.py:50-59 of the reference)
         torch.ops.orcasaq2.shard_gemm(x, lin["trellis"], lin["suh"], lin["svh"], oc, float(K), False, False)
 
     import orcasaq2.ops  # noqa: F401  (registers torch.ops.orcasaq2)
@@ -329,6 +333,8 @@ def config3_bench(reps: int) -> dict:
     t_gemm = _time_graph(gg, side, reps)
     gr, side_r = _graph(dev, recon)
     t_rec = _time_graph(gr, side_r, reps)
+    grt, side_rt = _graph(dev, recon_t)
+    t_rect = _time_graph(grt, side_rt, reps)
     op()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -349,10 +355,14 @@ def config3_bench(reps: int) -> dict:
                                       "TFLOP/s": round(flops / t_op / 1e12, 2),
                                       "mfma_util": round(flops / t_op / 1e12 / MFMA_F16_PEAK_TFS, 4),
                                       "what": "torch.ops.orcasaq2.shard_gemm at M=2048 (eager): had_r_128, "
-                                              "reconstruct, library fp16 GEMM, had_r_128"},
+                                              "reconstruct to (oc, ic), library fp16 transposed-B GEMM, "
+                                              "had_r_128"},
             "reconstruct": {"us_per_call": round(t_rec * 1e6, 2), "bytes": rbytes,
                             "GB/s": round(rbytes / t_rec / 1e9, 1),
-                            "frac": round(rbytes / t_rec / 1e9 / HBM_PEAK_GBS, 4)}}
+                            "frac": round(rbytes / t_rec / 1e9 / HBM_PEAK_GBS, 4)},
+            "reconstruct_t": {"us_per_call": round(t_rect * 1e6, 2), "bytes": rbytes,
+                              "GB/s": round(rbytes / t_rect / 1e9, 1),
+                              "frac": round(rbytes / t_rect / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
 def cpu_baseline(max_seconds: float = 30.0) -> dict:

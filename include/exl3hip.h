@@ -62,6 +62,15 @@ int exl3_abi_version(void);
 int exl3_reconstruct(void* W, const void* trellis, int ic, int oc, int K, int codebook, void* stream);
 
 /*
+ * Dense reconstruct, transposed: Wt (oc, ic) fp16 row-major, Wt[o][i] = W_q[i][o], from the
+ * same trellis.  No entry point of the reference writes this layout: it is the reference's
+ * reconstruct branch [orcasaq2/ops.py:54-59] made faster -- y = x W_q becomes a
+ * transposed-B library GEMM (y = x Wt^T), the library's faster layout on MI355X.  Same
+ * argument rules and bit-exactness as exl3_reconstruct.
+ */
+int exl3_reconstruct_t(void* Wt, const void* trellis, int ic, int oc, int K, int codebook, void* stream);
+
+/*
  * Block-128 Walsh-Hadamard along the last dim of a (rows, cols) fp16 matrix:
  *   out = ((in * pre) . blockdiag(H128 / sqrt(128))) * post * scale
  * pre/post are fp16 (cols) vectors or NULL; in == out is allowed.

@@ -56,7 +56,7 @@ extern "C" {
 
 const char* exl3_last_error(void) { return g_err; }
 
-int exl3_abi_version(void) { return 2; }
+int exl3_abi_version(void) { return 3; }
 
 int exl3_reconstruct(void* W, const void* trellis, int ic, int oc, int K, int codebook, void* stream)
 {
@@ -69,7 +69,22 @@ int exl3_reconstruct(void* W, const void* trellis, int ic, int oc, int K, int co
     int rc = check_codebook("exl3_reconstruct", codebook);
     if (rc) return rc;
     return reconstruct_dispatch(static_cast<uint16_t*>(W), static_cast<const uint32_t*>(trellis), ic, oc, K,
-                                codebook, static_cast<hipStream_t>(stream));
+                                codebook, false, static_cast<hipStream_t>(stream));
+}
+
+int exl3_reconstruct_t(void* Wt, const void* trellis, int ic, int oc, int K, int codebook, void* stream)
+{
+    g_err[0] = 0;
+    if (!Wt || !trellis) return set_error(EXL3_ERR_ARG, "exl3_reconstruct_t: null pointer");
+    if (ic <= 0 || oc <= 0 || ic % 16 || oc % 16)
+        return set_error(EXL3_ERR_ARG, "exl3_reconstruct_t: ic=%d and oc=%d must be positive multiples of 16", ic,
+                         oc);
+    if (!aligned(Wt, 16) || !aligned(trellis, 4))
+        return set_error(EXL3_ERR_ARG, "exl3_reconstruct_t: Wt must be 16-byte and trellis 4-byte aligned");
+    int rc = check_codebook("exl3_reconstruct_t", codebook);
+    if (rc) return rc;
+    return reconstruct_dispatch(static_cast<uint16_t*>(Wt), static_cast<const uint32_t*>(trellis), ic, oc, K,
+                                codebook, true, static_cast<hipStream_t>(stream));
 }
 
 int exl3_had_r_128(const void* in, void* out, const void* pre, const void* post, float scale, long rows, int cols,

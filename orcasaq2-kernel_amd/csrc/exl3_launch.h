@@ -15,7 +15,7 @@ int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3
 // Returns EXL3_OK, or records the pending launch error of `what`.
 int check_launch(const char* what);
 
-int reconstruct_dispatch(uint16_t* W, const uint32_t* trellis, int ic, int oc, int K, int cb,
+int reconstruct_dispatch(uint16_t* W, const uint32_t* trellis, int ic, int oc, int K, int cb, bool transposed,
                          hipStream_t stream);
 int had_dispatch(const uint16_t* in, uint16_t* out, const uint16_t* pre, const uint16_t* post,
                  float scale, long rows, int cols, hipStream_t stream);

@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libexl3hip.so"
 LIB_PATH = os.environ.get("ORCASAQ2_LIB", os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME))
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 CB_3INST, CB_MCG, CB_MUL1 = 0, 1, 2
 GEMV_MAX_ROWS = 16
@@ -38,6 +38,8 @@ _SIGS = {
     "exl3_abi_version": (ctypes.c_int, []),
     "exl3_reconstruct": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "exl3_reconstruct_t": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "exl3_had_r_128": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                       ctypes.c_float, ctypes.c_long, ctypes.c_int, ctypes.c_void_p]),
     "exl3_gemv_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
@@ -187,6 +189,21 @@ def reconstruct(trellis: torch.Tensor, K, codebook: int, out: torch.Tensor | Non
     _need(out.dtype == torch.float16 and out.is_contiguous() and tuple(out.shape) == (ic, oc), fn,
           "out must be contiguous fp16 (ic, oc)")
     _check(lib().exl3_reconstruct(_ptr(out), _ptr(trellis), ic, oc, K, codebook, _stream(dev)), fn)
+    return out
+
+
+def reconstruct_t(trellis: torch.Tensor, K, codebook: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """W_q^T (oc, ic) fp16 from the same trellis: the reconstruct branch's operand for a
+    transposed-B library GEMM (orcasaq2/ops.py:54-59 multiplies by W_q)."""
+    fn = "exl3_reconstruct_t"
+    dev = _need_gpu(fn, trellis, out)
+    ic, oc = trellis.shape[0] * 16, trellis.shape[1] * 16
+    K = check_trellis(fn, trellis, ic, oc, K)
+    if out is None:
+        out = torch.empty((oc, ic), dtype=torch.float16, device=dev)
+    _need(out.dtype == torch.float16 and out.is_contiguous() and tuple(out.shape) == (oc, ic), fn,
+          "out must be contiguous fp16 (oc, ic)")
+    _check(lib().exl3_reconstruct_t(_ptr(out), _ptr(trellis), ic, oc, K, codebook, _stream(dev)), fn)
     return out
 
 

@@ -74,6 +74,12 @@ def test_other_entry_points_reject_bad_arguments(native):
     assert L.exl3_reconstruct(fake, fake, 100, 256, 4, 0, None) == 1
     assert L.exl3_reconstruct(fake, fake, 256, 256, 0, 0, None) == 1
     assert L.exl3_reconstruct(P(0x10008), fake, 256, 256, 4, 0, None) == 1  # W not 16-aligned
+    assert L.exl3_reconstruct_t(fake, fake, 256, 100, 4, 0, None) == 1
+    assert "exl3_reconstruct_t" in _err(native) and "multiples of 16" in _err(native)
+    assert L.exl3_reconstruct_t(fake, fake, 256, 256, 9, 0, None) == 1
+    assert "K=9" in _err(native)
+    assert L.exl3_reconstruct_t(P(0x10008), fake, 256, 256, 4, 0, None) == 1
+    assert L.exl3_reconstruct_t(fake, fake, 256, 256, 4, 7, None) != 0      # unknown codebook
     assert L.exl3_had_r_128(fake, fake, None, None, 1.0, 4, 100, None) == 1
     assert L.exl3_gemm(fake, fake, fake, fake, fake, P(0x100000), 1 << 30, 0, 256, 256, 4, 0, None) == 1
     assert L.exl3_gemm(fake, fake, fake, fake, fake, P(0x100000), 8, 32, 256, 256, 4, 0, None) == 3

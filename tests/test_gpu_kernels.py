@@ -64,6 +64,30 @@ def test_reconstruct_bit_exact_config3_full(native, oracle):
     assert np.array_equal(u16(W), oracle.reconstruct(lin["trellis"], 4, 0))
 
 
+@pytest.mark.parametrize("K", range(1, 9))
+@pytest.mark.parametrize("cb", [0, 1])
+def test_reconstruct_t_bit_exact_small(native, oracle, K, cb):
+    """exl3_reconstruct_t writes W_q^T: the oracle's W_q transposed, bit for bit"""
+    lin = syn.linear(384, 256, K, seed=10 * K + cb + 5)
+    Wt = native.reconstruct_t(lin["trellis"].to(dev()), K, cb)
+    assert tuple(Wt.shape) == (256, 384)
+    assert np.array_equal(u16(Wt), oracle.reconstruct(lin["trellis"], K, cb).T)
+
+
+@pytest.mark.parametrize("ic,oc", [(16, 16), (208, 16), (144, 48), (1040, 32), (48, 1040)])
+def test_reconstruct_t_ragged_tile_counts(native, oracle, ic, oc):
+    """tile-row counts that are not multiples of the transposed kernel's 8-tile band"""
+    lin = syn.linear(ic, oc, 5, seed=ic + 3 * oc)
+    Wt = native.reconstruct_t(lin["trellis"].to(dev()), 5, 1)
+    assert np.array_equal(u16(Wt), oracle.reconstruct(lin["trellis"], 5, 1).T)
+
+
+def test_reconstruct_t_config3_full(native, oracle):
+    lin = syn.linear(17408, 5120, 4, seed=3)
+    Wt = native.reconstruct_t(lin["trellis"].to(dev()), 4, 0)
+    assert np.array_equal(u16(Wt), oracle.reconstruct(lin["trellis"], 4, 0).T)
+
+
 # ---------------------------------------------------------------- hadamard
 
 @pytest.mark.parametrize("pre,post,scale", [(False, False, 1.0), (True, False, 1.0), (False, True, 0.5),
