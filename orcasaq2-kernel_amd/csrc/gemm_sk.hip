@@ -1,5 +1,5 @@
-// EXL3 GEMM, stream-K over BM x 256 output tiles (BM = 256 for prefill, 16 for 2..16-row
-// decode batches):
+// EXL3 GEMM, stream-K over BM x 256 output tiles (BM = 64, 128 or 256 for prefill by row
+// count, 16 for 2..16-row decode batches):
 //   C = fp16( H( Ah . W_q ) * svh ),  Ah = fp16(H(A * suh)) (a had_r_128 pass)
 // W_q is decoded from the packed trellis straight into LDS (never written to HBM), once per
 // BM-row tile, and multiplied with v_mfma_f32_16x16x32_f16.  Replaces the reconstruct
@@ -16,7 +16,8 @@
 // tile) adds the slots in workgroup order -- deterministic -- and finishes the tile.
 //
 // Per workgroup (8 waves; BM = 256: wave w owns rows 128 (w / 4) .., outputs 64 (w % 4) ..,
-// 8 x 4 MFMA blocks; BM = 16: wave w owns outputs 32 w .., 1 x 2 blocks) and K-step:
+// 8 x 4 MFMA blocks; BM = 16/64/128: wave w owns all rows and outputs 32 w .., BM/16 x 2
+// blocks) and K-step:
 //   * the A tile (BM x 64 fp16) is loaded into registers one K-step ahead, then stored to
 //     LDS rows of 72 halves (16-byte reads of 16 consecutive rows hit distinct banks);
 //   * the B tile is 4 tile rows x 16 tile columns = 512 chunks of 32 positions, one per
@@ -43,15 +44,24 @@ struct SkCfg;
 template <>
 struct SkCfg<256> { static constexpr int WM = 2, WN = 4, MB = 8, NB = 4; };
 template <>
+struct SkCfg<128> { static constexpr int WM = 1, WN = 8, MB = 8, NB = 2; };
+template <>
+struct SkCfg<64> { static constexpr int WM = 1, WN = 8, MB = 4, NB = 2; };
+template <>
 struct SkCfg<16> { static constexpr int WM = 1, WN = 8, MB = 1, NB = 2; };
 
 template <int BM>
 constexpr int sk_acc() { return SkCfg<BM>::MB * SkCfg<BM>::NB * 4; }   // fp32 accumulators per lane
-// LDS of a launch: the A and B tiles of one K-step, twice for BM = 256 (the tiles of step
-// s + 1 are written while the MFMAs read those of step s), once for BM = 16 (three
-// workgroups per CU).
+// LDS of a launch: the A and B tiles of one K-step, twice for BM >= 128 (the tiles of step
+// s + 1 are written while the MFMAs read those of step s; one workgroup per CU), once for
+// BM <= 64 (several workgroups per CU overlap one another's phases instead).
 template <int BM>
-constexpr int sk_nbuf() { return BM == 256 ? 2 : 1; }
+constexpr int sk_nbuf() { return BM >= 128 ? 2 : 1; }
+// Waves per SIMD the register budget is set for, and workgroups per CU of a launch.
+template <int BM>
+constexpr int sk_wpe() { return BM >= 128 ? 2 : BM == 64 ? 4 : 6; }
+template <int BM>
+constexpr int sk_wgpc() { return BM >= 128 ? 1 : BM == 64 ? 2 : 3; }
 template <int BM>
 constexpr int sk_buf() { return (BM + SK_BN) * SK_LD; }                   // halves per A + B buffer
 template <int BM>
@@ -201,7 +211,7 @@ __device__ __forceinline__ void sk_load(uint32_t (&w)[K + 1], const uint32_t* __
 // K > 0: every shard of the launch has K bits per weight; K = 0: each tile piece takes its
 // shard's K (one launch for shards of different bit widths).
 template <int K, int CB, int BM>
-__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(BM == 256 ? 2 : 6, BM == 256 ? 2 : 6)))
+__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(sk_wpe<BM>(), sk_wpe<BM>())))
 void gemm_sk_kernel(const SkArgs a)
 {
     using Cfg = SkCfg<BM>;
@@ -390,31 +400,43 @@ void gemm_sk_kernel(const SkArgs a)
                 for (int mb = 0; mb < MB; mb++)
 #pragma unroll
                     for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+                // Slots in workgroup order, each read in batches of SK_RB 8-byte loads per lane
+                // that are all issued before the first add (atomic loads keep program order,
+                // so loads interleaved with the adds would have two in flight at a time).
+                constexpr int NP = MB * NB * 2;                   // 8-byte words per lane and slot
+                constexpr int RB = NP < 16 ? NP : 16;
                 for (int gg = g_lo; gg <= g_hi; gg++) {
                     const uint64_t* sl =
                         reinterpret_cast<const uint64_t*>(a.slots + ((long)(t + gg) * SK_WAVES + wave) * ACC * 64) + lane;
 #pragma unroll
-                    for (int mb = 0; mb < MB; mb++)
+                    for (int b0 = 0; b0 < NP; b0 += RB) {
+                        uint64_t v[RB];
 #pragma unroll
-                        for (int nb = 0; nb < NB; nb++) {
-                            const uint64_t p = __hip_atomic_load(sl + (long)((mb * NB + nb) * 2) * 64, __ATOMIC_RELAXED,
-                                                                 __HIP_MEMORY_SCOPE_AGENT);
-                            const uint64_t q = __hip_atomic_load(sl + (long)((mb * NB + nb) * 2 + 1) * 64,
-                                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                            acc[mb][nb] += f32x4{__builtin_bit_cast(float, (uint32_t)p),
-                                                 __builtin_bit_cast(float, (uint32_t)(p >> 32)),
-                                                 __builtin_bit_cast(float, (uint32_t)q),
-                                                 __builtin_bit_cast(float, (uint32_t)(q >> 32))};
+                        for (int i = 0; i < RB; i++)
+                            v[i] = __hip_atomic_load(sl + (long)(b0 + i) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                        for (int i = 0; i < RB; i += 2) {
+                            const int blk = (b0 + i) >> 1, mb = blk / NB, nb = blk % NB;
+                            acc[mb][nb] += f32x4{__builtin_bit_cast(float, (uint32_t)v[i]),
+                                                 __builtin_bit_cast(float, (uint32_t)(v[i] >> 32)),
+                                                 __builtin_bit_cast(float, (uint32_t)v[i + 1]),
+                                                 __builtin_bit_cast(float, (uint32_t)(v[i + 1] >> 32))};
                         }
+                    }
                 }
             }
         }
         if (finish) {
-            auto store_row = [&](int row, int ob, float v0, float v1) {
+            // svh pair of this lane in the 128-output block starting at tile column ob, read
+            // once per block: the fp16 output stores could alias it, so a load inside the
+            // row loop would be repeated (a round trip per row)
+            auto load_sv = [&](int ob) -> uint32_t {
+                return ob < tc ? reinterpret_cast<const uint32_t*>(S.svh + ob * 16)[lane] : 0u;
+            };
+            auto store_row = [&](int row, int ob, uint32_t sv, float v0, float v1) {
                 // ob: tile column of the 128-output block's first output
                 wave_fwht128(v0, v1);
                 if (ob < tc && row < a.rows) {
-                    const uint32_t sv = reinterpret_cast<const uint32_t*>(S.svh + ob * 16)[lane];
                     const float sv0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv & 0xffffu));
                     const float sv1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv >> 16));
                     const uint32_t o = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v0 * sv0)) |
@@ -428,7 +450,9 @@ void gemm_sk_kernel(const SkArgs a)
                 // 64-column halves.  16 rows at a time through LDS (16 x 132 floats per block
                 // and row half), then wave (wn & 1) transforms rows 8 (wn & 1) .. + 7.
                 const int blk = wn >> 1, half = wn & 1;
+                const uint32_t sv = load_sv(16 * tn + 8 * blk);
                 float* cs = reinterpret_cast<float*>(lds) + (wm * 2 + blk) * 16 * SK_CLD;
+#pragma unroll
                 for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
                     for (int nb = 0; nb < NB; nb++)
@@ -436,26 +460,34 @@ void gemm_sk_kernel(const SkArgs a)
                         for (int e = 0; e < 4; e++)
                             cs[(4 * (lane >> 4) + e) * SK_CLD + 64 * half + 16 * nb + (lane & 15)] = acc[mb][nb][e];
                     __syncthreads();
-                    for (int r = 8 * half; r < 8 * half + 8; r++)
-                        store_row(m0 + 128 * wm + 16 * mb + r, 16 * tn + 8 * blk, cs[r * SK_CLD + 2 * lane],
+#pragma unroll
+                    for (int r = 8 * half; r < 8 * half + 8; r++)   // eight independent transforms
+                        store_row(m0 + 128 * wm + 16 * mb + r, 16 * tn + 8 * blk, sv, cs[r * SK_CLD + 2 * lane],
                                   cs[r * SK_CLD + 2 * lane + 1]);
                     __syncthreads();
                 }
             } else {
-                // the whole 16 x 256 tile in LDS (16 rows of 260 floats); wave w transforms
-                // (row, block) pairs w, w + 8, w + 16, w + 24
+                // 16 rows at a time through LDS (16 rows of 260 floats); wave w transforms the
+                // chunk's (row, block) pairs w, w + 8, w + 16, w + 24
                 constexpr int LD = SK_BN + 4;
                 float* cs = reinterpret_cast<float*>(lds);
+                const uint32_t sv[2] = {load_sv(16 * tn), load_sv(16 * tn + 8)};
 #pragma unroll
-                for (int nb = 0; nb < NB; nb++)
+                for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        cs[(4 * (lane >> 4) + e) * LD + NB * 16 * wn + 16 * nb + (lane & 15)] = acc[0][nb][e];
-                __syncthreads();
-                for (int j = wave; j < 32; j += SK_WAVES) {
-                    const int r = j & 15, blk = j >> 4;
-                    store_row(m0 + r, 16 * tn + 8 * blk, cs[r * LD + 128 * blk + 2 * lane],
-                              cs[r * LD + 128 * blk + 2 * lane + 1]);
+                    for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++)
+                            cs[(4 * (lane >> 4) + e) * LD + NB * 16 * wn + 16 * nb + (lane & 15)] = acc[mb][nb][e];
+                    __syncthreads();
+#pragma unroll
+                    for (int jj = 0; jj < 4; jj++) {
+                        const int j = wave + SK_WAVES * jj;
+                        const int r = j & 15, blk = j >> 4;
+                        store_row(m0 + 16 * mb + r, 16 * tn + 8 * blk, sv[blk], cs[r * LD + 128 * blk + 2 * lane],
+                                  cs[r * LD + 128 * blk + 2 * lane + 1]);
+                    }
+                    if (mb + 1 < MB) __syncthreads();
                 }
             }
         }
@@ -475,9 +507,9 @@ int gemm_sk_cus()
     return cus;
 }
 
-// Workgroups per launch: BM = 256 keeps one per CU (two waves per SIMD), BM = 16 three.
+// Workgroups per launch: sk_wgpc per CU, all resident at once.
 template <int BM>
-static int sk_gmax() { return (BM == 256 ? 1 : 3) * gemm_sk_cus(); }
+static int sk_gmax() { return sk_wgpc<BM>() * gemm_sk_cus(); }
 
 template <int BM>
 static size_t sk_slot() { return (size_t)SK_WAVES * sk_acc<BM>() * 64 * sizeof(float); }
@@ -488,9 +520,33 @@ static int sk_ntn(int oc) { return (oc + SK_BN - 1) / SK_BN; }
 template <int BM>
 static size_t sk_ws(long tiles, int G) { return sk_align((size_t)tiles * 4) + (size_t)(tiles + G) * sk_slot<BM>(); }
 
-size_t gemm_sk_slot_bytes(int rows, int oc, int G)
+// Tile height of a prefill launch of `rows` rows.  Each weight is decoded once per row tile;
+// a taller tile pays that decode over more rows but MFMA work for padding rows and bigger
+// partial sums.  Measured on MI355X (17408 -> 5120, 5120 -> 17408, 5120 -> 6144): 64 is
+// fastest up to 64 rows, 128 up to 384 (two or three 128-row tiles beat one 256-row tile:
+// more tiles, fewer stream-K partial sums per tile), 256 above.
+static int gemm_sk_bm(int rows)
 {
-    return sk_ws<256>((long)((rows + 255) / 256) * sk_ntn(oc), G);
+#ifdef EXL3_SK_FORCE_BM
+    return EXL3_SK_FORCE_BM;
+#else
+    return rows <= 64 ? 64 : rows <= 384 ? 128 : 256;
+#endif
+}
+
+template <int BM>
+static size_t gemm_sk_ws(int rows, int oc)
+{
+    return sk_ws<BM>((long)((rows + BM - 1) / BM) * sk_ntn(oc), sk_gmax<BM>());
+}
+
+size_t gemm_sk_slot_bytes(int rows, int oc)
+{
+    switch (gemm_sk_bm(rows)) {
+    case 64: return gemm_sk_ws<64>(rows, oc);
+    case 128: return gemm_sk_ws<128>(rows, oc);
+    default: return gemm_sk_ws<256>(rows, oc);
+    }
 }
 
 // Per-shard workspace of the 2..16-row GEMV: its activations fp16(H(A * suh)), then its
@@ -553,9 +609,8 @@ static int sk_launch(SkArgs& a, int K, int cb, char* ws, size_t ws_bytes, const 
 }
 
 int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
-                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, int G, hipStream_t stream)
+                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream)
 {
-    (void)G;
     SkArgs a = {};
     a.rows = rows;
     a.ic = ic;
@@ -571,8 +626,13 @@ int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, c
     s.ntn = sk_ntn(oc);
     s.tbeg = 0;
     s.K = K;
-    a.ntiles = ((rows + 255) / 256) * s.ntn;
-    return sk_launch<256>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
+    const int bm = gemm_sk_bm(rows);
+    a.ntiles = ((rows + bm - 1) / bm) * s.ntn;
+    switch (bm) {
+    case 64: return sk_launch<64>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
+    case 128: return sk_launch<128>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
+    default: return sk_launch<256>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
+    }
 }
 
 // 2..16 rows: per codebook, groups of up to SK_MAXSH shards; per group one set-up kernel
