@@ -129,6 +129,19 @@ int exl3_gemm(const void* A, const void* trellis, void* C, const void* suh, cons
               void* stream);
 
 /*
+ * Grouped prefill GEMM: exl3_gemm for several shards that read the same A (the q/k/v of
+ * qkv_proj, gate/up of gate_up_proj), with exl3_gemv_grouped's shard table and output
+ * layout.  Per codebook one set-up kernel (every shard's Hadamard pass, the tile counters)
+ * and one stream-K launch over all the shards' tiles, whatever their K (up to 384 rows;
+ * above, one launch per K).  Replaces the per-shard loop of shard_gemm calls plus
+ * torch.cat at orcasaq2/config.py:237-243 for 17 .. GEMM_MAX_ROWS rows.  The workspace is
+ * exl3_gemm_grouped_workspace_bytes.
+ */
+size_t exl3_gemm_grouped_workspace_bytes(const exl3_shard_t* shards, int nshards, int rows, int ic);
+int exl3_gemm_grouped(const void* A, const exl3_shard_t* shards, int nshards, void* workspace,
+                      size_t ws_bytes, int rows, int ic, void* stream);
+
+/*
  * int8 embedding gather: out[n, :] = dtype(table[ids[n], :]) * scales[ids[n]], computed
  * in the scale dtype (0 = fp16, 1 = bf16, 2 = fp32); table (vocab, dim) int8 with
  * dim % 4 == 0, scales (vocab) or (vocab, 1), ids int64 (n_ids), out (n_ids, dim).

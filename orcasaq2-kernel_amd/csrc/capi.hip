@@ -56,7 +56,7 @@ extern "C" {
 
 const char* exl3_last_error(void) { return g_err; }
 
-int exl3_abi_version(void) { return 3; }
+int exl3_abi_version(void) { return 4; }
 
 int exl3_reconstruct(void* W, const void* trellis, int ic, int oc, int K, int codebook, void* stream)
 {
@@ -170,6 +170,47 @@ int exl3_gemm(const void* A, const void* trellis, void* C, const void* suh, cons
                          static_cast<uint16_t*>(C), static_cast<const uint16_t*>(suh),
                          static_cast<const uint16_t*>(svh), workspace, ws_bytes, rows, ic, oc, K, codebook,
                          static_cast<hipStream_t>(stream));
+}
+
+size_t exl3_gemm_grouped_workspace_bytes(const exl3_shard_t* shards, int nshards, int rows, int ic)
+{
+    if (!shards || nshards < 1 || rows < 1 || ic < 128) return 0;
+    size_t t = 0;
+    for (int i = 0; i < nshards; i++) {
+        if (shards[i].oc < 128) return 0;
+        t += gemm_grouped_shard_bytes(rows, ic, shards[i].oc);
+    }
+    return t;
+}
+
+int exl3_gemm_grouped(const void* A, const exl3_shard_t* shards, int nshards, void* workspace, size_t ws_bytes,
+                      int rows, int ic, void* stream)
+{
+    g_err[0] = 0;
+    if (!A || !shards || nshards < 1 || nshards > EXL3_MAX_SHARDS)
+        return set_error(EXL3_ERR_ARG, "exl3_gemm_grouped: need A and 1..%d shards (got %d)", EXL3_MAX_SHARDS,
+                         nshards);
+    if (!workspace) return set_error(EXL3_ERR_ARG, "exl3_gemm_grouped: null workspace");
+    if (rows < 1) return set_error(EXL3_ERR_ARG, "exl3_gemm_grouped: rows=%d", rows);
+    if (!aligned(A, 4) || !aligned(workspace, 256))
+        return set_error(EXL3_ERR_ARG, "exl3_gemm_grouped: A must be 4-byte and workspace 256-byte aligned");
+    const size_t need = exl3_gemm_grouped_workspace_bytes(shards, nshards, rows, ic);
+    GemvShard d[EXL3_MAX_SHARDS];
+    for (int i = 0; i < nshards; i++) {
+        const exl3_shard_t& s = shards[i];
+        int rc = check_linear("exl3_gemm_grouped", s.trellis, s.suh, s.svh, ic, s.oc, s.K, s.codebook);
+        if (rc) return rc;
+        if (!s.C || !aligned(s.C, 4) || s.ldc < s.oc || s.ldc % 2)
+            return set_error(EXL3_ERR_ARG, "exl3_gemm_grouped: shard %d: C must be 4-byte aligned with even ldc >= oc",
+                             i);
+        d[i] = GemvShard{static_cast<const uint32_t*>(s.trellis), static_cast<const uint16_t*>(s.suh),
+                         static_cast<const uint16_t*>(s.svh), static_cast<uint16_t*>(s.C), ic, s.oc, s.K,
+                         s.codebook, s.ldc};
+    }
+    if (ws_bytes < need)
+        return set_error(EXL3_ERR_WORKSPACE, "exl3_gemm_grouped: workspace of %zu bytes, %zu needed", ws_bytes, need);
+    return gemm_grouped_dispatch(static_cast<const uint16_t*>(A), d, nshards, rows, static_cast<char*>(workspace),
+                                 ws_bytes, static_cast<hipStream_t>(stream));
 }
 
 int exl3_embed_int8_gather(const void* table, const void* scales, int scale_dtype, const void* ids, void* out,

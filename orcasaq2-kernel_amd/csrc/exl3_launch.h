@@ -48,6 +48,9 @@ size_t gemm_sk_slot_bytes(int rows, int oc);
 size_t gemv_sk_bytes(int rows, int ic, int oc);
 int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws, size_t ws_bytes,
                      hipStream_t stream);
+size_t gemm_grouped_shard_bytes(int rows, int ic, int oc);
+int gemm_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws,
+                          size_t ws_bytes, hipStream_t stream);
 int gemm_sk_cus();
 int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
                      size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream);

@@ -91,7 +91,7 @@ __global__ void sk_clear_kernel(uint32_t* counters, int n)
     if (i < n) counters[i] = 0u;
 }
 
-// Set-up of a 2..16-row launch in one kernel: the tile counters to zero and, for every
+// Set-up of a grouped launch in one kernel: the tile counters to zero and, for every
 // shard, its activations Ah = fp16(H128(A * suh)) (rows x ic), one wave per (shard, row,
 // 128-input block).
 struct SkPrepArgs {
@@ -549,22 +549,31 @@ size_t gemm_sk_slot_bytes(int rows, int oc)
     }
 }
 
-// Per-shard workspace of the 2..16-row GEMV: its activations fp16(H(A * suh)), then its
-// share of counters and slots (each launch has at least one shard, so the shares cover it).
-size_t gemv_sk_bytes(int rows, int ic, int oc)
+// Per-shard workspace of a grouped launch (several shards reading the same A): the shard's
+// activations fp16(H(A * suh)), then its share of counters and slots (each launch has at
+// least one shard, so the shares cover it).
+template <int BM>
+static size_t sk_grouped_bytes(int rows, int ic, int oc)
 {
-    return sk_align((size_t)rows * ic * 2) + sk_ws<16>(sk_ntn(oc), sk_gmax<16>());
+    return sk_align((size_t)rows * ic * 2) + sk_ws<BM>((long)((rows + BM - 1) / BM) * sk_ntn(oc), sk_gmax<BM>());
 }
+
+size_t gemv_sk_bytes(int rows, int ic, int oc) { return sk_grouped_bytes<16>(rows, ic, oc); }
 
 template <int K, int CB, int BM>
 static const void* sk_fn() { return reinterpret_cast<const void*>(&gemm_sk_kernel<K, CB, BM>); }
+
+// The per-piece-K kernel (K = 0) exists for BM <= 128; a mixed-K group of 256-row tiles
+// is launched once per K instead.
+template <int BM>
+constexpr bool sk_has_k0() { return BM <= 128; }
 
 template <int BM>
 static const void* sk_fn_kcb(int K, int cb)
 {
 #define EXL3_CASE(KK) case KK: return cb == CB_MCG ? sk_fn<KK, CB_MCG, BM>() : sk_fn<KK, CB_3INST, BM>();
-    if constexpr (BM == 16)
-        if (K == 0) return cb == CB_MCG ? sk_fn<0, CB_MCG, 16>() : sk_fn<0, CB_3INST, 16>();   // per-shard K
+    if constexpr (sk_has_k0<BM>())
+        if (K == 0) return cb == CB_MCG ? sk_fn<0, CB_MCG, BM>() : sk_fn<0, CB_3INST, BM>();   // per-shard K
     switch (K) {
         EXL3_CASE(1) EXL3_CASE(2) EXL3_CASE(3) EXL3_CASE(4)
         EXL3_CASE(5) EXL3_CASE(6) EXL3_CASE(7) EXL3_CASE(8)
@@ -635,13 +644,16 @@ int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, c
     }
 }
 
-// 2..16 rows: per codebook, groups of up to SK_MAXSH shards; per group one set-up kernel
-// (the shards' activations, the group's tile counters) and one stream-K launch with 16-row
-// tiles -- a single-K kernel when the group's shards share K, else the per-shard-K one.
-int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws, size_t ws_bytes,
-                     hipStream_t stream)
+// Shards that read the same A (rows x ic): per codebook (and per K where no per-piece-K
+// kernel exists), groups of up to SK_MAXSH shards; per group one set-up kernel (the
+// shards' activations, the group's tile counters) and one stream-K launch -- a single-K
+// kernel when the group's shards share K, else the per-shard-K one.
+template <int BM>
+static int sk_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws,
+                               size_t ws_bytes, const char* what, hipStream_t stream)
 {
     const int ic = shards[0].ic;
+    const int nrb = (rows + BM - 1) / BM;
     bool done[EXL3_MAX_SHARDS] = {false};
     size_t off = 0;
     const size_t ah = sk_align((size_t)rows * ic * 2);
@@ -657,10 +669,11 @@ int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, in
         int tiles = 0, K = shards[i].K;
         for (int s = i; s < nshards && a.nshards < SK_MAXSH; s++) {
             if (done[s] || shards[s].cb != shards[i].cb) continue;
+            if (!sk_has_k0<BM>() && shards[s].K != shards[i].K) continue;
             const GemvShard& d = shards[s];
-            if (d.K < 1 || d.K > 8) return set_error(EXL3_ERR_ARG, "exl3_gemv: K=%d is not in 1..8", d.K);
+            if (d.K < 1 || d.K > 8) return set_error(EXL3_ERR_ARG, "%s: K=%d is not in 1..8", what, d.K);
             if (off + ah > ws_bytes)
-                return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: workspace of %zu bytes is too small", ws_bytes);
+                return set_error(EXL3_ERR_WORKSPACE, "%s: workspace of %zu bytes is too small", what, ws_bytes);
             uint16_t* Ah = reinterpret_cast<uint16_t*>(ws + off);
             off += ah;
             p.suh[a.nshards] = d.suh;
@@ -676,23 +689,51 @@ int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, in
             e.tbeg = tiles;
             e.K = d.K;
             if (d.K != K) K = 0;
-            tiles += e.ntn;
+            tiles += nrb * e.ntn;
             done[s] = true;
         }
         a.ntiles = p.ntiles = tiles;
         p.nsh = a.nshards;
         p.counters = reinterpret_cast<uint32_t*>(ws + off);
-        const int waves = std::max(p.nsh * rows * p.nblk, tiles);
-        hipLaunchKernelGGL(sk_prep_kernel, dim3((waves + 3) / 4), dim3(256), 0, stream, p);
-        int rc = check_launch("exl3_gemv (set-up)");
+        const long waves = std::max<long>((long)p.nsh * rows * p.nblk, tiles);
+        hipLaunchKernelGGL(sk_prep_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, p);
+        int rc = check_launch(what);
         if (rc != EXL3_OK) return rc;
-        const size_t need = sk_ws<16>(tiles, sk_gmax<16>());
+        const size_t need = sk_ws<BM>(tiles, sk_gmax<BM>());
         const size_t avail = ws_bytes > off ? ws_bytes - off : 0;
-        rc = sk_launch<16>(a, K, shards[i].cb, ws + off, std::min(need, avail), "exl3_gemv", stream, false);
+        rc = sk_launch<BM>(a, K, shards[i].cb, ws + off, std::min(need, avail), what, stream, false);
         if (rc != EXL3_OK) return rc;
         off += std::min(need, avail);
     }
     return EXL3_OK;
+}
+
+// 2..16 rows: 16-row tiles.
+int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws, size_t ws_bytes,
+                     hipStream_t stream)
+{
+    return sk_grouped_dispatch<16>(A, shards, nshards, rows, ws, ws_bytes, "exl3_gemv", stream);
+}
+
+// Prefill of several shards (exl3_gemm_grouped): tile height by rows, as for one shard.
+size_t gemm_grouped_shard_bytes(int rows, int ic, int oc)
+{
+    switch (gemm_sk_bm(rows)) {
+    case 64: return sk_grouped_bytes<64>(rows, ic, oc);
+    case 128: return sk_grouped_bytes<128>(rows, ic, oc);
+    default: return sk_grouped_bytes<256>(rows, ic, oc);
+    }
+}
+
+int gemm_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws,
+                          size_t ws_bytes, hipStream_t stream)
+{
+    const char* what = "exl3_gemm_grouped";
+    switch (gemm_sk_bm(rows)) {
+    case 64: return sk_grouped_dispatch<64>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
+    case 128: return sk_grouped_dispatch<128>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
+    default: return sk_grouped_dispatch<256>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
+    }
 }
 
 }  // namespace exl3

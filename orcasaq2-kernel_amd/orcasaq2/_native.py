@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libexl3hip.so"
 LIB_PATH = os.environ.get("ORCASAQ2_LIB", os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME))
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 CB_3INST, CB_MCG, CB_MUL1 = 0, 1, 2
 GEMV_MAX_ROWS = 16
@@ -55,6 +55,11 @@ _SIGS = {
     "exl3_gemm": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
                                  ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "exl3_gemm_grouped_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(Shard), ctypes.c_int,
+                                                            ctypes.c_int, ctypes.c_int]),
+    "exl3_gemm_grouped": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Shard), ctypes.c_int,
+                                         ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_void_p]),
     "exl3_embed_int8_gather": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_long,
                                               ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
@@ -229,17 +234,10 @@ def had_r_128(x: torch.Tensor, out: torch.Tensor | None = None, pre: torch.Tenso
     return out
 
 
-def gemv_grouped(x: torch.Tensor, shards: list[dict], out: torch.Tensor | None = None) -> torch.Tensor:
-    """Fused decode-GEMV of 1..16 rows through one or more shards that share x; returns
-    (rows, sum oc) with the shards' outputs side by side (the concat of
-    orcasaq2/config.py:243 written in place).  Each shard: dict(trellis, suh, svh, oc, K,
-    codebook)."""
-    fn = "exl3_gemv"
-    _need(x.dim() == 2, fn, "x must be (rows, ic)")
+def _shard_table(fn: str, x: torch.Tensor, shards: list[dict], out: torch.Tensor | None, dev):
+    """(out, exl3_shard_t array) of a grouped call: the shards' outputs side by side in out
+    (rows, sum oc), shard s writing its columns with row stride sum oc."""
     rows, ic = x.shape
-    dev = _need_gpu(fn, x, out, *[s["trellis"] for s in shards])
-    _need(x.dtype == torch.float16 and x.is_contiguous(), fn, "x must be contiguous fp16")
-    _need(1 <= rows <= GEMV_MAX_ROWS, fn, f"rows={rows} is not in 1..{GEMV_MAX_ROWS}")
     _need(1 <= len(shards) <= MAX_SHARDS, fn, f"{len(shards)} shards")
     total = sum(int(s["oc"]) for s in shards)
     if out is None:
@@ -256,6 +254,21 @@ def gemv_grouped(x: torch.Tensor, shards: list[dict], out: torch.Tensor | None =
         arr[i] = Shard(s["trellis"].data_ptr(), s["suh"].data_ptr(), s["svh"].data_ptr(),
                        out.data_ptr() + 2 * col, total, oc, K, int(s["codebook"]))
         col += oc
+    return out, arr
+
+
+def gemv_grouped(x: torch.Tensor, shards: list[dict], out: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused decode-GEMV of 1..16 rows through one or more shards that share x; returns
+    (rows, sum oc) with the shards' outputs side by side (the concat of
+    orcasaq2/config.py:243 written in place).  Each shard: dict(trellis, suh, svh, oc, K,
+    codebook)."""
+    fn = "exl3_gemv"
+    _need(x.dim() == 2, fn, "x must be (rows, ic)")
+    rows, ic = x.shape
+    dev = _need_gpu(fn, x, out, *[s["trellis"] for s in shards])
+    _need(x.dtype == torch.float16 and x.is_contiguous(), fn, "x must be contiguous fp16")
+    _need(1 <= rows <= GEMV_MAX_ROWS, fn, f"rows={rows} is not in 1..{GEMV_MAX_ROWS}")
+    out, arr = _shard_table(fn, x, shards, out, dev)
     L = lib()
     nbytes = L.exl3_gemv_grouped_workspace_bytes(arr, len(shards), rows, ic)
     ws = gemv_workspace(dev, nbytes)
@@ -297,6 +310,26 @@ def gemm(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.T
 
 
 _SCALE_DTYPES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def gemm_grouped(x: torch.Tensor, shards: list[dict], out: torch.Tensor | None = None) -> torch.Tensor:
+    """Prefill of several shards that share x in one stream-K launch per codebook: returns
+    (rows, sum oc) with the shards' outputs side by side (the concat of
+    orcasaq2/config.py:243 written in place).  Each shard: dict(trellis, suh, svh, oc, K,
+    codebook)."""
+    fn = "exl3_gemm_grouped"
+    _need(x.dim() == 2, fn, "x must be (rows, ic)")
+    rows, ic = x.shape
+    dev = _need_gpu(fn, x, out, *[s["trellis"] for s in shards])
+    _need(x.dtype == torch.float16 and x.is_contiguous(), fn, "x must be contiguous fp16")
+    out, arr = _shard_table(fn, x, shards, out, dev)
+    if rows == 0:
+        return out
+    L = lib()
+    nbytes = L.exl3_gemm_grouped_workspace_bytes(arr, len(shards), rows, ic)
+    ws = workspace(dev, nbytes)
+    _check(L.exl3_gemm_grouped(_ptr(x), arr, len(shards), _ptr(ws), nbytes, rows, ic, _stream(dev)), fn)
+    return out
 
 
 def embed_int8(table: torch.Tensor, scales: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:

@@ -15,6 +15,7 @@ from ._vllm_compat import (
     QuantizeMethodBase,
     init_logger,
 )
+from . import ops as _ops
 from .ops import GEMV_MAX_ROWS, exl3_K  # noqa: F401  (importing ops registers the custom ops)
 
 logger = init_logger(__name__)
@@ -220,7 +221,8 @@ class Exl3LinearMethod(LinearMethodBase):
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
         """fp16 activations through every shard, outputs concatenated in slot order, cast
         back to x.dtype, plus bias (orcasaq2/config.py:228-245).  A multi-shard layer at
-        <= 16 rows runs as one grouped op that writes the concat in place."""
+        <= GEMM_MAX_ROWS rows runs as one grouped op (decode-GEMV up to 16 rows, stream-K
+        GEMM above) that writes the concat in place."""
         if layer.exl3_shards is None:
             out = torch.nn.functional.linear(x, layer.exl3_dense.to(x.dtype))
             return out + bias if bias is not None else out
@@ -229,8 +231,9 @@ class Exl3LinearMethod(LinearMethodBase):
         if not xf.is_contiguous():
             xf = xf.contiguous()
         shards = layer.exl3_shards
-        if len(shards) > 1 and 0 < rows <= GEMV_MAX_ROWS:
-            out = torch.ops.orcasaq2.shards_gemv(
+        if len(shards) > 1 and 0 < rows <= _ops.GEMM_MAX_ROWS:
+            grouped = torch.ops.orcasaq2.shards_gemv if rows <= GEMV_MAX_ROWS else torch.ops.orcasaq2.shards_gemm
+            out = grouped(
                 xf, [s["trellis"] for s in shards], [s["suh"] for s in shards],
                 [s["svh"] for s in shards], [s["oc"] for s in shards],
                 [float(s["K"]) for s in shards], [s["mcg"] for s in shards],

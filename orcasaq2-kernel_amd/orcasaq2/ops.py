@@ -90,3 +90,20 @@ def shards_gemv(x: Tensor, trellis: list[Tensor], suh: list[Tensor], svh: list[T
 @shards_gemv.register_fake
 def _shards_gemv_fake(x, trellis, suh, svh, oc, k, mcg, mul1) -> Tensor:
     return x.new_empty((x.shape[0], sum(oc)), dtype=torch.half)
+
+
+@torch.library.custom_op("orcasaq2::shards_gemm", mutates_args=(), device_types="cuda")
+def shards_gemm(x: Tensor, trellis: list[Tensor], suh: list[Tensor], svh: list[Tensor],
+                oc: list[int], k: list[float], mcg: list[bool], mul1: list[bool]) -> Tensor:
+    """All shards of a fused layer for 16 < rows <= GEMM_MAX_ROWS: one set-up kernel (each
+    shard's Hadamard pass) and one stream-K launch per codebook for all of them, outputs
+    side by side -- the per-shard shard_gemm loop + torch.cat of orcasaq2/config.py:237-243
+    with one launch tail instead of one per shard."""
+    shards = [dict(trellis=t, suh=a, svh=b, oc=o, K=kk, codebook=_native.codebook_id(m, m1))
+              for t, a, b, o, kk, m, m1 in zip(trellis, suh, svh, oc, k, mcg, mul1)]
+    return _native.gemm_grouped(x, shards)
+
+
+@shards_gemm.register_fake
+def _shards_gemm_fake(x, trellis, suh, svh, oc, k, mcg, mul1) -> Tensor:
+    return x.new_empty((x.shape[0], sum(oc)), dtype=torch.half)

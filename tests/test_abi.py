@@ -19,8 +19,8 @@ def header_functions():
 
 def test_header_lists_the_entry_points():
     fns = header_functions()
-    for f in ("exl3_reconstruct", "exl3_had_r_128", "exl3_gemv", "exl3_gemv_grouped", "exl3_gemm",
-              "exl3_embed_int8_gather", "exl3_last_error"):
+    for f in ("exl3_reconstruct", "exl3_reconstruct_t", "exl3_had_r_128", "exl3_gemv", "exl3_gemv_grouped",
+              "exl3_gemm", "exl3_gemm_grouped", "exl3_embed_int8_gather", "exl3_last_error"):
         assert f in fns
 
 
@@ -86,6 +86,18 @@ def test_other_entry_points_reject_bad_arguments(native):
     assert L.exl3_embed_int8_gather(fake, fake, 0, fake, fake, 4, 100, 10, None) == 1  # dim % 4
     assert L.exl3_embed_int8_gather(fake, fake, 5, fake, fake, 4, 100, 16, None) == 1  # dtype
     assert L.exl3_embed_int8_gather(None, None, 0, None, None, 0, 0, 16, None) == 0    # empty: no-op
+    sh = (native.Shard * 2)()
+    sh[0] = native.Shard(0x10000, 0x10000, 0x10000, 0x10000, 512, 256, 4, 0)
+    sh[1] = native.Shard(0x10000, 0x10000, 0x10000, 0x10100, 512, 256, 5, 0)
+    assert L.exl3_gemm_grouped(fake, sh, 0, P(0x100000), 1 << 30, 32, 256, None) == 1      # no shards
+    assert L.exl3_gemm_grouped(fake, sh, 2, P(0x100000), 1 << 30, 0, 256, None) == 1       # rows
+    assert L.exl3_gemm_grouped(fake, sh, 2, P(0x100000), 8, 32, 256, None) == 3            # workspace
+    assert "exl3_gemm_grouped" in _err(native) and "needed" in _err(native)
+    sh[1] = native.Shard(0x10000, 0x10000, 0x10000, 0x10100, 100, 256, 5, 0)
+    assert L.exl3_gemm_grouped(fake, sh, 2, P(0x100000), 1 << 30, 32, 256, None) == 1     # ldc < oc
+    assert "shard 1" in _err(native)
+    assert L.exl3_gemm_grouped_workspace_bytes(sh, 2, 32, 256) > 0
+    assert L.exl3_gemm_grouped_workspace_bytes(sh, 2, 0, 256) == 0
 
 
 def test_workspace_sizes(native):

@@ -249,13 +249,45 @@ def test_gemm_K(native, oracle, K, cb):
 @pytest.mark.parametrize("rows,ic,oc,K,cb", [(257, 128, 128, 3, 0), (300, 640, 640, 4, 1), (520, 1024, 384, 2, 0),
                                           (700, 256, 1152, 5, 0), (450, 384, 256, 8, 0)])
 def test_gemm_streamk_shapes(native, oracle, rows, ic, oc, K, cb):
-    """above 192 rows: 256 x 256 tiles split over workgroups by K-steps (ragged rows, output
-    counts that leave half a tile, tiny ic, both codebooks)"""
+    """128-row tiles (up to 384 rows) and 256-row tiles (above) split over workgroups by
+    K-steps: ragged rows, output counts that leave half a tile, tiny ic, both codebooks"""
     lin = syn.linear(ic, oc, K, seed=rows + oc)
     x = syn.activations(rows, ic, torch.Generator().manual_seed(rows))
     d = to_gpu(lin)
     y = native.gemm(x.to(dev()), d["trellis"], d["suh"], d["svh"], K, cb)
     check_linear_out(y, x, lin, cb, oracle)
+
+
+@pytest.mark.parametrize("rows", [17, 64, 100, 200, 450])
+def test_gemm_grouped_mixed_K_and_codebooks(native, oracle, rows):
+    """exl3_gemm_grouped: shards of several K (interleaved) and both codebooks that read one
+    A; 64- and 128-row tiles take each codebook's shards in one launch (per-piece K), 256-row
+    tiles one launch per K.  Deterministic across calls."""
+    spec = [(384, 3, 0), (256, 5, 0), (128, 3, 1), (640, 2, 0), (256, 3, 0), (128, 6, 1), (384, 5, 0)]
+    x = syn.activations(rows, 768, torch.Generator().manual_seed(50 + rows))
+    lins = [syn.linear(768, oc, K, seed=500 + i) for i, (oc, K, _) in enumerate(spec)]
+    shards = [dict(to_gpu(l), codebook=cb) for l, (_, _, cb) in zip(lins, spec)]
+    y = native.gemm_grouped(x.to(dev()), shards)
+    col = 0
+    for l, (_, _, cb) in zip(lins, spec):
+        check_linear_out(y[:, col:col + l["oc"]], x, l, cb, oracle)
+        col += l["oc"]
+    assert torch.equal(native.gemm_grouped(x.to(dev()), shards), y)
+
+
+@pytest.mark.parametrize("rows", [40, 144])
+def test_gemm_grouped_config2(native, oracle, rows):
+    """qkv (q K4 5120->6144, k/v K5 5120->1024) and gate_up (2 x K3 5120->17408) prefill
+    through one grouped launch each; oracle on every row"""
+    x = syn.activations(rows, 5120, torch.Generator().manual_seed(60 + rows))
+    for spec in ([(6144, 4), (1024, 5), (1024, 5)], [(17408, 3), (17408, 3)]):
+        lins = [syn.linear(5120, oc, K, seed=600 + i) for i, (oc, K) in enumerate(spec)]
+        shards = [dict(to_gpu(l), codebook=0) for l in lins]
+        y = native.gemm_grouped(x.to(dev()), shards)
+        col = 0
+        for l in lins:
+            check_linear_out(y[:, col:col + l["oc"]], x, l, 0, oracle)
+            col += l["oc"]
 
 
 def test_gemm_streamk_deterministic(native):

@@ -1,4 +1,4 @@
-"""GPU tests of the drop-in surface: the orcasaq2::shard_gemm / shards_gemv custom ops
+"""GPU tests of the drop-in surface: the orcasaq2::shard_gemm / shards_gemv / shards_gemm custom ops
 (all three row branches), HIP-graph capture and replay, torch.compile around the op,
 and Exl3LinearMethod.apply through a stand-in vLLM layer."""
 import numpy as np
@@ -50,21 +50,22 @@ def test_shard_gemm_wrong_width_message(native):
         torch.ops.orcasaq2.shard_gemm(x, lin["trellis"], lin["suh"], lin["svh"], 256, 3.0, False, False)
 
 
-@pytest.mark.parametrize("rows", [1, 2, 9])
+@pytest.mark.parametrize("rows", [1, 2, 9, 40])
 def test_hip_graph_capture_replays(native, oracle, rows):
     """The op and the grouped op captured into a HIP graph and replayed four times, with
     eager work between replays, against eager results: 1 row (persistent kernel, its
     counters rearmed by every call), 2 rows (four-row template), 9 rows (16-row tiles,
-    one launch over both K)."""
+    one launch over both K), 40 rows (prefill: 64-row stream-K tiles, counters zeroed by
+    the set-up kernels inside the graph)."""
     lins = [syn.linear(1024, oc, K, seed=i) for i, (oc, K) in enumerate([(512, 4), (256, 5)])]
     ds = [on(l) for l in lins]
     x = syn.activations(rows, 1024, torch.Generator().manual_seed(1)).to(D)
 
     def step():
         a = torch.ops.orcasaq2.shard_gemm(x, ds[0]["trellis"], ds[0]["suh"], ds[0]["svh"], 512, 4.0, False, False)
-        b = torch.ops.orcasaq2.shards_gemv(x, [d["trellis"] for d in ds], [d["suh"] for d in ds],
-                                           [d["svh"] for d in ds], [512, 256], [4.0, 5.0], [False, False],
-                                           [False, False])
+        grouped = torch.ops.orcasaq2.shards_gemv if rows <= 16 else torch.ops.orcasaq2.shards_gemm
+        b = grouped(x, [d["trellis"] for d in ds], [d["suh"] for d in ds], [d["svh"] for d in ds], [512, 256],
+                    [4.0, 5.0], [False, False], [False, False])
         return a, b
 
     eager = step()
@@ -99,8 +100,9 @@ def test_torch_compile_treats_op_as_opaque(native):
 
 
 def test_linear_method_apply_fused_layers(native, oracle):
-    """qkv_proj-style layer: shards captured by slot, processed, applied (grouped op at
-    <= 16 rows, per-shard ops + cat above), bias added, dtype restored."""
+    """qkv_proj-style layer: shards captured by slot, processed, applied (grouped decode-GEMV
+    at <= 16 rows, grouped GEMM to 144, per-shard ops + cat above), bias added, dtype
+    restored."""
     from orcasaq2.config import Exl3Config, Exl3LinearMethod
     from orcasaq2._vllm_compat import LinearBase
     cfg = Exl3Config.from_config({"bits": 4})
@@ -116,7 +118,7 @@ def test_linear_method_apply_fused_layers(native, oracle):
     layer.bias.data = torch.randn(768).to(torch.bfloat16)
     layer.quant_method.process_weights_after_loading(layer)
     layer.bias.data = layer.bias.data.to(D)
-    for rows in (1, 5, 40):
+    for rows in (1, 5, 40, 144, 200):
         x = syn.activations(rows, 256, torch.Generator().manual_seed(rows)).to(torch.bfloat16)
         y = layer(x.to(D))
         assert y.dtype == torch.bfloat16 and y.shape == (rows, 768)

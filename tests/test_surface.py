@@ -20,16 +20,28 @@ from orcasaq2.ops import exl3_K
 
 @pytest.fixture(scope="module")
 def cpu_ops(oracle):
+    """Oracle-backed CPU kernels for the custom ops (host-logic tests only); `calls` records
+    which op each call reached."""
+    calls = []
+
     def one(x, trellis, suh, svh, oc, k, mcg, mul1):
         y = oracle.shard_gemm_ref(x.numpy(), trellis.numpy(), suh.numpy(), svh.numpy(), int(k), 1 if mcg else 0)
         return torch.from_numpy(y).to(torch.half)
 
-    def many(x, trellis, suh, svh, oc, k, mcg, mul1):
-        return torch.cat([one(x, *a) for a in zip(trellis, suh, svh, oc, k, mcg, mul1)], dim=1)
+    def single(*a):
+        calls.append("shard_gemm")
+        return one(*a)
 
-    torch.library.register_kernel("orcasaq2::shard_gemm", "cpu", one)
-    torch.library.register_kernel("orcasaq2::shards_gemv", "cpu", many)
-    return one
+    def many(name):
+        def run(x, trellis, suh, svh, oc, k, mcg, mul1):
+            calls.append(name)
+            return torch.cat([one(x, *a) for a in zip(trellis, suh, svh, oc, k, mcg, mul1)], dim=1)
+        return run
+
+    torch.library.register_kernel("orcasaq2::shard_gemm", "cpu", single)
+    torch.library.register_kernel("orcasaq2::shards_gemv", "cpu", many("shards_gemv"))
+    torch.library.register_kernel("orcasaq2::shards_gemm", "cpu", many("shards_gemm"))
+    return calls
 
 
 def test_exl3_K_matches_reference_semantics():
@@ -90,9 +102,14 @@ def test_fused_layer_apply_matches_oracle(cpu_ops, oracle):
     assert [s["K"] for s in layer.exl3_shards] == [4, 5, 5]
     assert all(s["suh"].dtype == torch.half for s in layer.exl3_shards)
     layer.bias.data = torch.randn(512)
-    for rows in (1, 3, 20):
+    # grouped decode-GEMV to 16 rows, grouped GEMM to GEMM_MAX_ROWS (144), per shard above
+    route = {1: ["shards_gemv"], 3: ["shards_gemv"], 20: ["shards_gemm"], 144: ["shards_gemm"],
+             145: ["shard_gemm"] * 3}
+    for rows, want in route.items():
         x = torch.randn(rows, 128)
+        cpu_ops.clear()
         y = layer(x)
+        assert cpu_ops == want, (rows, cpu_ops)
         assert y.dtype == torch.float32 and y.shape == (rows, 512)
         col = 0
         for sid, oc, K in spec:
