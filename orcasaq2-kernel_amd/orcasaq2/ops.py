@@ -13,8 +13,9 @@ Dispatch on the number of activation rows (reference: orcasaq2/ops.py:25, 46-59)
                           keep enough workgroups resident); rows 5..16: stream-K over 16-row
                           tiles; output Hadamard and svh in the last step;
   * 16 < rows <= GEMM_MAX_ROWS
-                          fused decode-GEMM (exl3_gemm): Hadamard pass over x, then tiles
-                          decoded straight into MFMA operands, output Hadamard in the epilogue;
+                          fused decode-GEMM (exl3_gemm): Hadamard pass over x, then stream-K
+                          tiles decoded straight into MFMA operands, output Hadamard in the
+                          epilogue; a fused layer's shards together (shards_gemm);
   * rows > GEMM_MAX_ROWS  the reference's reconstruct branch: had_r_128(x, suh), dense W_q
                           (decoded transposed, (oc, ic)) into a scratch freed on exit, library
                           fp16 transposed-B GEMM, had_r_128(y, svh).
