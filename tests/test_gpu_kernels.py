@@ -275,6 +275,19 @@ def test_gemm_grouped_mixed_K_and_codebooks(native, oracle, rows):
     assert torch.equal(native.gemm_grouped(x.to(dev()), shards), y)
 
 
+def test_gemm_grouped_more_shards_than_one_launch(native, oracle):
+    """10 shards of one codebook: two launches (8 shards per launch), each with its own
+    set-up kernel and workspace share"""
+    x = syn.activations(33, 256, torch.Generator().manual_seed(70))
+    lins = [syn.linear(256, 128 * (1 + i % 3), 2 + i % 4, seed=700 + i) for i in range(10)]
+    shards = [dict(to_gpu(l), codebook=0) for l in lins]
+    y = native.gemm_grouped(x.to(dev()), shards)
+    col = 0
+    for l in lins:
+        check_linear_out(y[:, col:col + l["oc"]], x, l, 0, oracle)
+        col += l["oc"]
+
+
 @pytest.mark.parametrize("rows", [40, 144])
 def test_gemm_grouped_config2(native, oracle, rows):
     """qkv (q K4 5120->6144, k/v K5 5120->1024) and gate_up (2 x K3 5120->17408) prefill
