@@ -29,6 +29,7 @@ embedding gather of one batch-1 token as one HIP graph, replayed (attention excl
     python bench.py --workload config2   # grouped qkv / gate_up GEMVs at batch 1, 4, 16
     python bench.py --workload config3   # M=2048 prefill GEMM (TFLOP/s, MFMA share) + reconstruct
     python bench.py --workload config4   # the 64-layer batch-1 linear stack alone (tok/s-equivalent)
+    python bench.py --workload prefill   # 17..768-row prefill: fused vs reconstruct branch, grouped layers
 print their own JSON line instead of the headline line.
 """
 from __future__ import annotations
@@ -207,6 +208,53 @@ def _time_graph(graph, side, reps: int) -> float:
     e1.record(side)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def prefill_bench(reps: int) -> dict:
+    """Prefill at few rows (17..768), the 27B layer shapes: per shape and row count the fused
+    stream-K GEMM (exl3_gemm) against the op's reconstruct branch (had_r_128, reconstruct
+    to (oc, ic), library fp16 transposed-B GEMM, had_r_128); per fused layer (qkv, gate_up)
+    the grouped launch (exl3_gemm_grouped) against the per-shard fused GEMMs + cat and the
+    per-shard reconstruct branch + cat.  us per call, each call one HIP-graph replay."""
+    import torch
+    from orcasaq2 import _native
+    import orcasaq2.ops  # noqa: F401
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(5)
+
+    def t_of(fn):
+        graph, side = _graph(dev, fn)
+        return round(_time_graph(graph, side, reps) * 1e6, 1)
+
+    def recon(x, d):
+        xh = _native.had_r_128(x, pre=d["suh"])
+        y = torch.nn.functional.linear(xh, _native.reconstruct_t(d["trellis"], d["K"], 0))
+        return _native.had_r_128(y, out=y, post=d["svh"])
+
+    out = {"single": {}, "grouped": {}}
+    for name, ic, oc, K in (("down 17408->5120 K4", 17408, 5120, 4), ("gate 5120->17408 K3", 5120, 17408, 3),
+                            ("q 5120->6144 K4", 5120, 6144, 4)):
+        d = _rand_linear(ic, oc, K, g, dev)
+        row = {}
+        for M in (17, 64, 128, 144, 256, 384, 768):
+            x = torch.randn(M, ic, generator=g, device=dev).half()
+            y = torch.empty(M, oc, dtype=torch.half, device=dev)
+            row[M] = {"fused": t_of(lambda: _native.gemm(x, d["trellis"], d["suh"], d["svh"], K, 0, out=y)),
+                      "reconstruct_branch": t_of(lambda: recon(x, d))}
+        out["single"][name] = row
+    for name, spec in (("qkv (q 6144 K4, k/v 1024 K5)", [(6144, 4), (1024, 5), (1024, 5)]),
+                       ("gate_up (2 x 17408 K3)", [(17408, 3), (17408, 3)])):
+        sh = [_rand_linear(5120, o, k, g, dev) for o, k in spec]
+        row = {}
+        for M in (17, 64, 144):
+            x = torch.randn(M, 5120, generator=g, device=dev).half()
+            row[M] = {"grouped": t_of(lambda: _native.gemm_grouped(x, sh)),
+                      "per_shard_fused_cat": t_of(lambda: torch.cat(
+                          [_native.gemm(x, d["trellis"], d["suh"], d["svh"], d["K"], 0) for d in sh], dim=1)),
+                      "per_shard_reconstruct_cat": t_of(lambda: torch.cat([recon(x, d) for d in sh], dim=1))}
+        out["grouped"][name] = row
+    return out
 
 
 def stack_bench(tokens: int = 20) -> dict:
@@ -425,7 +473,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-K", type=int, default=0, help="time a single K (profiling runs)")
     ap.add_argument("--copy-calib", action="store_true", help="run the counter-calibration copy and exit")
-    ap.add_argument("--workload", default="config1", choices=("config1", "config2", "config3", "config4"),
+    ap.add_argument("--workload", default="config1", choices=("config1", "config2", "config3", "config4", "prefill"),
                     help="config1 = the headline line (+ the config-4 stack); config2/config3/config4 "
                          "print their own measurement line")
     ap.add_argument("--no-stack", action="store_true", help="skip the config-4 stack measurement")
@@ -438,10 +486,11 @@ def main():
     if args.copy_calib:
         copy_calib(args)
         return
-    if args.workload in ("config2", "config3", "config4"):
+    if args.workload in ("config2", "config3", "config4", "prefill"):
         import torch
         res = (config2_bench(args.steps * 5) if args.workload == "config2" else
-               config3_bench(args.steps) if args.workload == "config3" else stack_bench(args.steps))
+               config3_bench(args.steps) if args.workload == "config3" else
+               prefill_bench(args.steps) if args.workload == "prefill" else stack_bench(args.steps))
         print(json.dumps({"workload": args.workload, "results": res,
                           "device": torch.cuda.get_device_name(0)}), flush=True)
         return
