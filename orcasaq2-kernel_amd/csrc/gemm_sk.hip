@@ -52,16 +52,18 @@ struct SkCfg<16> { static constexpr int WM = 1, WN = 8, MB = 1, NB = 2; };
 
 template <int BM>
 constexpr int sk_acc() { return SkCfg<BM>::MB * SkCfg<BM>::NB * 4; }   // fp32 accumulators per lane
-// LDS of a launch: the A and B tiles of one K-step, twice for BM >= 128 (the tiles of step
+// LDS of a launch: the A and B tiles of one K-step, twice for BM >= 64 (the tiles of step
 // s + 1 are written while the MFMAs read those of step s; one workgroup per CU), once for
-// BM <= 64 (several workgroups per CU overlap one another's phases instead).
+// BM = 16 (three workgroups per CU overlap one another's phases instead).  Measured on
+// MI355X at 17..64 rows: the two-buffer pipeline with one workgroup per CU beats one buffer
+// with two workgroups per CU by 28% on 17408 -> 5120 and 6% on 5120 -> 17408.
 template <int BM>
-constexpr int sk_nbuf() { return BM >= 128 ? 2 : 1; }
+constexpr int sk_nbuf() { return BM >= 64 ? 2 : 1; }
 // Waves per SIMD the register budget is set for, and workgroups per CU of a launch.
 template <int BM>
-constexpr int sk_wpe() { return BM >= 128 ? 2 : BM == 64 ? 4 : 6; }
+constexpr int sk_wpe() { return BM >= 64 ? 2 : 6; }
 template <int BM>
-constexpr int sk_wgpc() { return BM >= 128 ? 1 : BM == 64 ? 2 : 3; }
+constexpr int sk_wgpc() { return BM >= 64 ? 1 : 3; }
 template <int BM>
 constexpr int sk_buf() { return (BM + SK_BN) * SK_LD; }                   // halves per A + B buffer
 template <int BM>
