@@ -37,6 +37,7 @@ constexpr int SK_KS = 64;                     // inputs per K-step (4 tile rows)
 constexpr int SK_LD = SK_KS + 8;              // halves per LDS row of the A and B tiles
 constexpr int SK_CLD = 128 + 4;               // floats per epilogue row in LDS (BM = 256)
 constexpr int SK_MAXSH = 8;                   // shards per launch
+constexpr int SK_PIPE16 = 24;                 // 16-row launches up to this many K-steps per CU: two buffers
 
 // Wave grid of a BM x 256 tile: WM x WN waves, each MB x NB blocks of 16 x 16.
 template <int BM>
@@ -57,17 +58,18 @@ constexpr int sk_acc() { return SkCfg<BM>::MB * SkCfg<BM>::NB * 4; }   // fp32 a
 // BM = 16 (three workgroups per CU overlap one another's phases instead).  Measured on
 // MI355X at 17..64 rows: the two-buffer pipeline with one workgroup per CU beats one buffer
 // with two workgroups per CU by 28% on 17408 -> 5120 and 6% on 5120 -> 17408.
+// A 16-row launch takes either form (NBUF = 1 or 2, chosen by its length).
 template <int BM>
 constexpr int sk_nbuf() { return BM >= 64 ? 2 : 1; }
 // Waves per SIMD the register budget is set for, and workgroups per CU of a launch.
-template <int BM>
-constexpr int sk_wpe() { return BM >= 64 ? 2 : 6; }
-template <int BM>
-constexpr int sk_wgpc() { return BM >= 64 ? 1 : 3; }
+template <int BM, int NBUF>
+constexpr int sk_wpe() { return NBUF == 2 ? 2 : 6; }
+template <int BM, int NBUF>
+constexpr int sk_wgpc() { return NBUF == 2 ? 1 : 3; }
 template <int BM>
 constexpr int sk_buf() { return (BM + SK_BN) * SK_LD; }                   // halves per A + B buffer
-template <int BM>
-constexpr int sk_lds() { return sk_nbuf<BM>() * sk_buf<BM>() * 2; }      // bytes
+template <int BM, int NBUF>
+constexpr int sk_lds() { return NBUF * sk_buf<BM>() * 2; }      // bytes
 
 struct SkShard {
     const uint16_t* Ah;        // (rows, ic) fp16, fp16(H(A * suh)) of this shard
@@ -212,8 +214,8 @@ __device__ __forceinline__ void sk_load(uint32_t (&w)[K + 1], const uint32_t* __
 
 // K > 0: every shard of the launch has K bits per weight; K = 0: each tile piece takes its
 // shard's K (one launch for shards of different bit widths).
-template <int K, int CB, int BM>
-__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(sk_wpe<BM>(), sk_wpe<BM>())))
+template <int K, int CB, int BM, int NBUF>
+__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(sk_wpe<BM, NBUF>(), sk_wpe<BM, NBUF>())))
 void gemm_sk_kernel(const SkArgs a)
 {
     using Cfg = SkCfg<BM>;
@@ -318,7 +320,7 @@ void gemm_sk_kernel(const SkArgs a)
 
 
             load_step(s0);
-            if constexpr (sk_nbuf<BM>() == 2) {
+            if constexpr (NBUF == 2) {
                 // Software pipeline over two LDS buffers, one barrier per K-step: during step s the
                 // MFMAs read buffer (s - s0) % 2 while the step s + 1 tiles (loaded into registers
                 // a step earlier) are decoded into the other buffer and step s + 2 is loaded.  The
@@ -510,8 +512,8 @@ int gemm_sk_cus()
 }
 
 // Workgroups per launch: sk_wgpc per CU, all resident at once.
-template <int BM>
-static int sk_gmax() { return sk_wgpc<BM>() * gemm_sk_cus(); }
+template <int BM, int NBUF = sk_nbuf<BM>()>
+static int sk_gmax() { return sk_wgpc<BM, NBUF>() * gemm_sk_cus(); }
 
 template <int BM>
 static size_t sk_slot() { return (size_t)SK_WAVES * sk_acc<BM>() * 64 * sizeof(float); }
@@ -562,20 +564,20 @@ static size_t sk_grouped_bytes(int rows, int ic, int oc)
 
 size_t gemv_sk_bytes(int rows, int ic, int oc) { return sk_grouped_bytes<16>(rows, ic, oc); }
 
-template <int K, int CB, int BM>
-static const void* sk_fn() { return reinterpret_cast<const void*>(&gemm_sk_kernel<K, CB, BM>); }
+template <int K, int CB, int BM, int NBUF>
+static const void* sk_fn() { return reinterpret_cast<const void*>(&gemm_sk_kernel<K, CB, BM, NBUF>); }
 
 // The per-piece-K kernel (K = 0) exists for BM <= 128; a mixed-K group of 256-row tiles
 // is launched once per K instead.
 template <int BM>
 constexpr bool sk_has_k0() { return BM <= 128; }
 
-template <int BM>
+template <int BM, int NBUF>
 static const void* sk_fn_kcb(int K, int cb)
 {
-#define EXL3_CASE(KK) case KK: return cb == CB_MCG ? sk_fn<KK, CB_MCG, BM>() : sk_fn<KK, CB_3INST, BM>();
+#define EXL3_CASE(KK) case KK: return cb == CB_MCG ? sk_fn<KK, CB_MCG, BM, NBUF>() : sk_fn<KK, CB_3INST, BM, NBUF>();
     if constexpr (sk_has_k0<BM>())
-        if (K == 0) return cb == CB_MCG ? sk_fn<0, CB_MCG, BM>() : sk_fn<0, CB_3INST, BM>();   // per-shard K
+        if (K == 0) return cb == CB_MCG ? sk_fn<0, CB_MCG, BM, NBUF>() : sk_fn<0, CB_3INST, BM, NBUF>();   // per-shard K
     switch (K) {
         EXL3_CASE(1) EXL3_CASE(2) EXL3_CASE(3) EXL3_CASE(4)
         EXL3_CASE(5) EXL3_CASE(6) EXL3_CASE(7) EXL3_CASE(8)
@@ -586,13 +588,13 @@ static const void* sk_fn_kcb(int K, int cb)
 
 // One stream-K launch over a.sh[0 .. nshards): clears its tile counters, then runs.  `ws`
 // holds the counters and slots (sk_ws bytes).
-template <int BM>
+template <int BM, int NBUF = sk_nbuf<BM>()>
 static int sk_launch(SkArgs& a, int K, int cb, char* ws, size_t ws_bytes, const char* what, hipStream_t stream,
                      bool clear = true)
 {
     const long units = (long)a.ntiles * a.nks;
     // at least 8 K-steps per workgroup: a tile has at most nks / 8 + 2 contributors
-    int G = (int)std::min<long>(sk_gmax<BM>(), std::max<long>(1, units / 8));
+    int G = (int)std::min<long>(sk_gmax<BM, NBUF>(), std::max<long>(1, units / 8));
     const size_t cbytes = sk_align((size_t)a.ntiles * 4);
     const long fit = ws_bytes > cbytes ? (long)((ws_bytes - cbytes) / sk_slot<BM>()) - a.ntiles : 0;
     if (fit < 1)
@@ -608,14 +610,14 @@ static int sk_launch(SkArgs& a, int K, int cb, char* ws, size_t ws_bytes, const 
         const int rc = check_launch(what);
         if (rc != EXL3_OK) return rc;
     }
-    const void* fn = sk_fn_kcb<BM>(K, cb);
+    const void* fn = sk_fn_kcb<BM, NBUF>(K, cb);
     if (!fn) return set_error(EXL3_ERR_ARG, "%s: K=%d is not in 1..8", what, K);   // K = 0: per shard
-    if (sk_lds<BM>() > 64 * 1024) {
-        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, sk_lds<BM>());
+    if (sk_lds<BM, NBUF>() > 64 * 1024) {
+        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, sk_lds<BM, NBUF>());
         (void)hipGetLastError();
     }
     void* kargs[] = {&a};
-    hipLaunchKernel(fn, dim3(G), dim3(64 * SK_WAVES), kargs, sk_lds<BM>(), stream);
+    hipLaunchKernel(fn, dim3(G), dim3(64 * SK_WAVES), kargs, sk_lds<BM, NBUF>(), stream);
     return check_launch(what);
 }
 
@@ -703,7 +705,18 @@ static int sk_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int n
         if (rc != EXL3_OK) return rc;
         const size_t need = sk_ws<BM>(tiles, sk_gmax<BM>());
         const size_t avail = ws_bytes > off ? ws_bytes - off : 0;
-        rc = sk_launch<BM>(a, K, shards[i].cb, ws + off, std::min(need, avail), what, stream, false);
+        // 16-row tiles: a short launch (at most SK_PIPE16 K-steps per CU) takes the two-buffer
+        // pipeline with one workgroup per CU, a longer one three single-buffer workgroups
+        // per CU (measured on MI355X at 16 rows: qkv, ~10 K-steps per CU, 31 -> 26 us;
+        // gate_up, ~42 per CU, 56 -> 62 us with two buffers)
+        if constexpr (BM == 16) {
+            if ((long)tiles * a.nks <= (long)SK_PIPE16 * gemm_sk_cus())
+                rc = sk_launch<16, 2>(a, K, shards[i].cb, ws + off, std::min(need, avail), what, stream, false);
+            else
+                rc = sk_launch<16, 1>(a, K, shards[i].cb, ws + off, std::min(need, avail), what, stream, false);
+        } else {
+            rc = sk_launch<BM>(a, K, shards[i].cb, ws + off, std::min(need, avail), what, stream, false);
+        }
         if (rc != EXL3_OK) return rc;
         off += std::min(need, avail);
     }
