@@ -1,5 +1,5 @@
-// EXL3 GEMM, stream-K over BM x 256 output tiles (BM = 64, 128 or 256 for prefill by row
-// count, 16 for 2..16-row decode batches):
+// EXL3 GEMM, stream-K over BM x 256 output tiles (BM = 32, 64, 128 or 256 for prefill by
+// row count, 16 for 5..16-row decode batches):
 //   C = fp16( H( Ah . W_q ) * svh ),  Ah = fp16(H(A * suh)) (a had_r_128 pass)
 // W_q is decoded from the packed trellis straight into LDS (never written to HBM), once per
 // BM-row tile, and multiplied with v_mfma_f32_16x16x32_f16.  Replaces the reconstruct
@@ -16,7 +16,7 @@
 // tile) adds the slots in workgroup order -- deterministic -- and finishes the tile.
 //
 // Per workgroup (8 waves; BM = 256: wave w owns rows 128 (w / 4) .., outputs 64 (w % 4) ..,
-// 8 x 4 MFMA blocks; BM = 16/64/128: wave w owns all rows and outputs 32 w .., BM/16 x 2
+// 8 x 4 MFMA blocks; BM = 16/32/64/128: wave w owns all rows and outputs 32 w .., BM/16 x 2
 // blocks) and K-step:
 //   * the A tile (BM x 64 fp16) is loaded into registers one K-step ahead, then stored to
 //     LDS rows of 72 halves (16-byte reads of 16 consecutive rows hit distinct banks);
@@ -49,18 +49,20 @@ struct SkCfg<128> { static constexpr int WM = 1, WN = 8, MB = 8, NB = 2; };
 template <>
 struct SkCfg<64> { static constexpr int WM = 1, WN = 8, MB = 4, NB = 2; };
 template <>
+struct SkCfg<32> { static constexpr int WM = 1, WN = 8, MB = 2, NB = 2; };
+template <>
 struct SkCfg<16> { static constexpr int WM = 1, WN = 8, MB = 1, NB = 2; };
 
 template <int BM>
 constexpr int sk_acc() { return SkCfg<BM>::MB * SkCfg<BM>::NB * 4; }   // fp32 accumulators per lane
-// LDS of a launch: the A and B tiles of one K-step, twice for BM >= 64 (the tiles of step
+// LDS of a launch: the A and B tiles of one K-step, twice for BM >= 32 (the tiles of step
 // s + 1 are written while the MFMAs read those of step s; one workgroup per CU), once for
 // BM = 16 (three workgroups per CU overlap one another's phases instead).  Measured on
 // MI355X at 17..64 rows: the two-buffer pipeline with one workgroup per CU beats one buffer
 // with two workgroups per CU by 28% on 17408 -> 5120 and 6% on 5120 -> 17408.
 // A 16-row launch takes either form (NBUF = 1 or 2, chosen by its length).
 template <int BM>
-constexpr int sk_nbuf() { return BM >= 64 ? 2 : 1; }
+constexpr int sk_nbuf() { return BM >= 32 ? 2 : 1; }
 // Waves per SIMD the register budget is set for, and workgroups per CU of a launch.
 template <int BM, int NBUF>
 constexpr int sk_wpe() { return NBUF == 2 ? 2 : 6; }
@@ -526,15 +528,16 @@ static size_t sk_ws(long tiles, int G) { return sk_align((size_t)tiles * 4) + (s
 
 // Tile height of a prefill launch of `rows` rows.  Each weight is decoded once per row tile;
 // a taller tile pays that decode over more rows but MFMA work for padding rows and bigger
-// partial sums.  Measured on MI355X (17408 -> 5120, 5120 -> 17408, 5120 -> 6144): 64 is
-// fastest up to 64 rows, 128 up to 384 (two or three 128-row tiles beat one 256-row tile:
-// more tiles, fewer stream-K partial sums per tile), 256 above.
+// partial sums.  Measured on MI355X (17408 -> 5120, 5120 -> 17408, 5120 -> 6144): 32 is
+// fastest up to 32 rows (13-22% below 64-row tiles), 64 up to 64, 128 up to 384 (two or
+// three 128-row tiles beat one 256-row tile: more tiles, fewer stream-K partial sums per
+// tile), 256 above.
 static int gemm_sk_bm(int rows)
 {
 #ifdef EXL3_SK_FORCE_BM
     return EXL3_SK_FORCE_BM;
 #else
-    return rows <= 64 ? 64 : rows <= 384 ? 128 : 256;
+    return rows <= 32 ? 32 : rows <= 64 ? 64 : rows <= 384 ? 128 : 256;
 #endif
 }
 
@@ -547,6 +550,7 @@ static size_t gemm_sk_ws(int rows, int oc)
 size_t gemm_sk_slot_bytes(int rows, int oc)
 {
     switch (gemm_sk_bm(rows)) {
+    case 32: return gemm_sk_ws<32>(rows, oc);
     case 64: return gemm_sk_ws<64>(rows, oc);
     case 128: return gemm_sk_ws<128>(rows, oc);
     default: return gemm_sk_ws<256>(rows, oc);
@@ -642,6 +646,7 @@ int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, c
     const int bm = gemm_sk_bm(rows);
     a.ntiles = ((rows + bm - 1) / bm) * s.ntn;
     switch (bm) {
+    case 32: return sk_launch<32>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
     case 64: return sk_launch<64>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
     case 128: return sk_launch<128>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
     default: return sk_launch<256>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
@@ -734,6 +739,7 @@ int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, in
 size_t gemm_grouped_shard_bytes(int rows, int ic, int oc)
 {
     switch (gemm_sk_bm(rows)) {
+    case 32: return sk_grouped_bytes<32>(rows, ic, oc);
     case 64: return sk_grouped_bytes<64>(rows, ic, oc);
     case 128: return sk_grouped_bytes<128>(rows, ic, oc);
     default: return sk_grouped_bytes<256>(rows, ic, oc);
@@ -745,6 +751,7 @@ int gemm_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshard
 {
     const char* what = "exl3_gemm_grouped";
     switch (gemm_sk_bm(rows)) {
+    case 32: return sk_grouped_dispatch<32>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
     case 64: return sk_grouped_dispatch<64>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
     case 128: return sk_grouped_dispatch<128>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
     default: return sk_grouped_dispatch<256>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
