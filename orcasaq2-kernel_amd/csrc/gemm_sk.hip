@@ -1,4 +1,4 @@
-// EXL3 GEMM, stream-K over BM x 256 output tiles (BM = 32, 64, 128 or 256 for prefill by
+// EXL3 GEMM, stream-K over BM x 256 output tiles (BM = 32, 48, 64, 128 or 256 for prefill by
 // row count, 16 for 5..16-row decode batches):
 //   C = fp16( H( Ah . W_q ) * svh ),  Ah = fp16(H(A * suh)) (a had_r_128 pass)
 // W_q is decoded from the packed trellis straight into LDS (never written to HBM), once per
@@ -16,7 +16,7 @@
 // tile) adds the slots in workgroup order -- deterministic -- and finishes the tile.
 //
 // Per workgroup (8 waves; BM = 256: wave w owns rows 128 (w / 4) .., outputs 64 (w % 4) ..,
-// 8 x 4 MFMA blocks; BM = 16/32/64/128: wave w owns all rows and outputs 32 w .., BM/16 x 2
+// 8 x 4 MFMA blocks; BM = 16..128: wave w owns all rows and outputs 32 w .., BM/16 x 2
 // blocks) and K-step:
 //   * the A tile (BM x 64 fp16) is loaded into registers one K-step ahead, then stored to
 //     LDS rows of 72 halves (16-byte reads of 16 consecutive rows hit distinct banks);
@@ -48,6 +48,8 @@ template <>
 struct SkCfg<128> { static constexpr int WM = 1, WN = 8, MB = 8, NB = 2; };
 template <>
 struct SkCfg<64> { static constexpr int WM = 1, WN = 8, MB = 4, NB = 2; };
+template <>
+struct SkCfg<48> { static constexpr int WM = 1, WN = 8, MB = 3, NB = 2; };
 template <>
 struct SkCfg<32> { static constexpr int WM = 1, WN = 8, MB = 2, NB = 2; };
 template <>
@@ -529,7 +531,8 @@ static size_t sk_ws(long tiles, int G) { return sk_align((size_t)tiles * 4) + (s
 // Tile height of a prefill launch of `rows` rows.  Each weight is decoded once per row tile;
 // a taller tile pays that decode over more rows but MFMA work for padding rows and bigger
 // partial sums.  Measured on MI355X (17408 -> 5120, 5120 -> 17408, 5120 -> 6144): 32 is
-// fastest up to 32 rows (13-22% below 64-row tiles), 64 up to 64, 128 up to 384 (two or
+// fastest up to 32 rows (13-22% below 64-row tiles), 48 up to 48 (8-15% below), 64 up to
+// 64, 128 up to 384 (two or
 // three 128-row tiles beat one 256-row tile: more tiles, fewer stream-K partial sums per
 // tile), 256 above.
 static int gemm_sk_bm(int rows)
@@ -537,7 +540,7 @@ static int gemm_sk_bm(int rows)
 #ifdef EXL3_SK_FORCE_BM
     return EXL3_SK_FORCE_BM;
 #else
-    return rows <= 32 ? 32 : rows <= 64 ? 64 : rows <= 384 ? 128 : 256;
+    return rows <= 32 ? 32 : rows <= 48 ? 48 : rows <= 64 ? 64 : rows <= 384 ? 128 : 256;
 #endif
 }
 
@@ -551,6 +554,7 @@ size_t gemm_sk_slot_bytes(int rows, int oc)
 {
     switch (gemm_sk_bm(rows)) {
     case 32: return gemm_sk_ws<32>(rows, oc);
+    case 48: return gemm_sk_ws<48>(rows, oc);
     case 64: return gemm_sk_ws<64>(rows, oc);
     case 128: return gemm_sk_ws<128>(rows, oc);
     default: return gemm_sk_ws<256>(rows, oc);
@@ -647,6 +651,7 @@ int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, c
     a.ntiles = ((rows + bm - 1) / bm) * s.ntn;
     switch (bm) {
     case 32: return sk_launch<32>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
+    case 48: return sk_launch<48>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
     case 64: return sk_launch<64>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
     case 128: return sk_launch<128>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
     default: return sk_launch<256>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
@@ -740,6 +745,7 @@ size_t gemm_grouped_shard_bytes(int rows, int ic, int oc)
 {
     switch (gemm_sk_bm(rows)) {
     case 32: return sk_grouped_bytes<32>(rows, ic, oc);
+    case 48: return sk_grouped_bytes<48>(rows, ic, oc);
     case 64: return sk_grouped_bytes<64>(rows, ic, oc);
     case 128: return sk_grouped_bytes<128>(rows, ic, oc);
     default: return sk_grouped_bytes<256>(rows, ic, oc);
@@ -752,6 +758,7 @@ int gemm_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshard
     const char* what = "exl3_gemm_grouped";
     switch (gemm_sk_bm(rows)) {
     case 32: return sk_grouped_dispatch<32>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
+    case 48: return sk_grouped_dispatch<48>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
     case 64: return sk_grouped_dispatch<64>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
     case 128: return sk_grouped_dispatch<128>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
     default: return sk_grouped_dispatch<256>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
