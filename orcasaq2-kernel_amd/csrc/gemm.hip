@@ -5,7 +5,7 @@
 // rows, with: one had_r_128 pass over A into the workspace, then the stream-K kernel of
 // gemm_sk.hip, which decodes trellis tiles straight into LDS as MFMA operands -- the dense
 // W_q is never written to HBM -- and applies the output Hadamard and svh in its epilogue.
-// The tile height follows the row count (32, 48, 64, 128 or 256 rows: gemm_sk.hip).
+// The tile height follows the row count (32, 48, 64, 96, 128 or 256 rows: gemm_sk.hip).
 #include "exl3_common.h"
 #include "exl3_launch.h"
 

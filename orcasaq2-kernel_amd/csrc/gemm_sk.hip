@@ -1,4 +1,4 @@
-// EXL3 GEMM, stream-K over BM x 256 output tiles (BM = 32, 48, 64, 128 or 256 for prefill by
+// EXL3 GEMM, stream-K over BM x 256 output tiles (BM = 32, 48, 64, 96, 128 or 256 for prefill by
 // row count, 16 for 5..16-row decode batches):
 //   C = fp16( H( Ah . W_q ) * svh ),  Ah = fp16(H(A * suh)) (a had_r_128 pass)
 // W_q is decoded from the packed trellis straight into LDS (never written to HBM), once per
@@ -48,6 +48,8 @@ template <>
 struct SkCfg<128> { static constexpr int WM = 1, WN = 8, MB = 8, NB = 2; };
 template <>
 struct SkCfg<64> { static constexpr int WM = 1, WN = 8, MB = 4, NB = 2; };
+template <>
+struct SkCfg<96> { static constexpr int WM = 1, WN = 8, MB = 6, NB = 2; };
 template <>
 struct SkCfg<48> { static constexpr int WM = 1, WN = 8, MB = 3, NB = 2; };
 template <>
@@ -237,8 +239,8 @@ void gemm_sk_kernel(const SkArgs a)
 
     // A-tile loader: thread t moves 16 bytes of row t / 8 (+ 64 p), segment t % 8.
     const int arow = tid >> 3, aseg = tid & 7;
-    constexpr int AP = BM >= 64 ? BM / 64 : 1;       // passes
-    const bool aload = BM >= 64 || arow < BM;
+    constexpr int AP = (BM + 63) / 64;               // passes; pass p moves rows 64 p + arow < BM
+    auto aload = [&](int p) { return 64 * p + arow < BM; };
     // B chunk of this thread: chunk id tid = 8 * tile + c, tile = 16 ti_l + tn_l (a tile's
     // 8 chunks on 8 consecutive lanes)
     const int c = lane & 7;
@@ -279,7 +281,7 @@ void gemm_sk_kernel(const SkArgs a)
 #pragma unroll
                 for (int p = 0; p < AP; p++) {
                     const int row = m0 + 64 * p + arow;
-                    areg[p] = (aload && row < a.rows)
+                    areg[p] = (aload(p) && row < a.rows)
                         ? *reinterpret_cast<const uint4*>(S.Ah + (long)row * a.ic + s * SK_KS + aseg * 8)
                         : uint4{0u, 0u, 0u, 0u};
                 }
@@ -292,7 +294,7 @@ void gemm_sk_kernel(const SkArgs a)
                 _Float16* bs = Bs(b);
 #pragma unroll
                 for (int p = 0; p < AP; p++)
-                    if (aload) *reinterpret_cast<uint4*>(as + (64 * p + arow) * SK_LD + aseg * 8) = areg[p];
+                    if (aload(p)) *reinterpret_cast<uint4*>(as + (64 * p + arow) * SK_LD + aseg * 8) = areg[p];
                 chunk_prev_dpp<KK>(w, first_lane);
                 uint4 o[4];
                 sk_decode<KK, CB>(w, kc, o);
@@ -532,7 +534,7 @@ static size_t sk_ws(long tiles, int G) { return sk_align((size_t)tiles * 4) + (s
 // a taller tile pays that decode over more rows but MFMA work for padding rows and bigger
 // partial sums.  Measured on MI355X (17408 -> 5120, 5120 -> 17408, 5120 -> 6144): 32 is
 // fastest up to 32 rows (13-22% below 64-row tiles), 48 up to 48 (8-15% below), 64 up to
-// 64, 128 up to 384 (two or
+// 64, 96 up to 96 (4-9% below 128-row tiles), 128 up to 384 (two or
 // three 128-row tiles beat one 256-row tile: more tiles, fewer stream-K partial sums per
 // tile), 256 above.
 static int gemm_sk_bm(int rows)
@@ -540,7 +542,7 @@ static int gemm_sk_bm(int rows)
 #ifdef EXL3_SK_FORCE_BM
     return EXL3_SK_FORCE_BM;
 #else
-    return rows <= 32 ? 32 : rows <= 48 ? 48 : rows <= 64 ? 64 : rows <= 384 ? 128 : 256;
+    return rows <= 32 ? 32 : rows <= 48 ? 48 : rows <= 64 ? 64 : rows <= 96 ? 96 : rows <= 384 ? 128 : 256;
 #endif
 }
 
@@ -555,6 +557,7 @@ size_t gemm_sk_slot_bytes(int rows, int oc)
     switch (gemm_sk_bm(rows)) {
     case 32: return gemm_sk_ws<32>(rows, oc);
     case 48: return gemm_sk_ws<48>(rows, oc);
+    case 96: return gemm_sk_ws<96>(rows, oc);
     case 64: return gemm_sk_ws<64>(rows, oc);
     case 128: return gemm_sk_ws<128>(rows, oc);
     default: return gemm_sk_ws<256>(rows, oc);
@@ -652,6 +655,7 @@ int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, c
     switch (bm) {
     case 32: return sk_launch<32>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
     case 48: return sk_launch<48>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
+    case 96: return sk_launch<96>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
     case 64: return sk_launch<64>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
     case 128: return sk_launch<128>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
     default: return sk_launch<256>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
@@ -746,6 +750,7 @@ size_t gemm_grouped_shard_bytes(int rows, int ic, int oc)
     switch (gemm_sk_bm(rows)) {
     case 32: return sk_grouped_bytes<32>(rows, ic, oc);
     case 48: return sk_grouped_bytes<48>(rows, ic, oc);
+    case 96: return sk_grouped_bytes<96>(rows, ic, oc);
     case 64: return sk_grouped_bytes<64>(rows, ic, oc);
     case 128: return sk_grouped_bytes<128>(rows, ic, oc);
     default: return sk_grouped_bytes<256>(rows, ic, oc);
@@ -759,6 +764,7 @@ int gemm_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshard
     switch (gemm_sk_bm(rows)) {
     case 32: return sk_grouped_dispatch<32>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
     case 48: return sk_grouped_dispatch<48>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
+    case 96: return sk_grouped_dispatch<96>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
     case 64: return sk_grouped_dispatch<64>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
     case 128: return sk_grouped_dispatch<128>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
     default: return sk_grouped_dispatch<256>(A, shards, nshards, rows, ws, ws_bytes, what, stream);

@@ -228,7 +228,7 @@ def test_gemv_grouped_mixed_K_and_codebooks(native, oracle, rows):
 
 # ---------------------------------------------------------------- GEMM
 
-@pytest.mark.parametrize("rows", [1, 5, 17, 40, 64, 100, 144, 300])
+@pytest.mark.parametrize("rows", [1, 5, 17, 40, 64, 80, 100, 144, 300])
 def test_gemm_rows(native, oracle, rows):
     lin = syn.linear(512, 640, 4, seed=rows)
     x = syn.activations(rows, 512, torch.Generator().manual_seed(rows))
@@ -258,7 +258,7 @@ def test_gemm_streamk_shapes(native, oracle, rows, ic, oc, K, cb):
     check_linear_out(y, x, lin, cb, oracle)
 
 
-@pytest.mark.parametrize("rows", [1, 5, 17, 40, 64, 100, 200, 450])
+@pytest.mark.parametrize("rows", [1, 5, 17, 40, 64, 80, 100, 200, 450])
 def test_gemm_grouped_mixed_K_and_codebooks(native, oracle, rows):
     """exl3_gemm_grouped: shards of several K (interleaved) and both codebooks that read one
     A; 64- and 128-row tiles take each codebook's shards in one launch (per-piece K), 256-row
