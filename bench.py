@@ -237,7 +237,7 @@ def prefill_bench(reps: int) -> dict:
                             ("q 5120->6144 K4", 5120, 6144, 4)):
         d = _rand_linear(ic, oc, K, g, dev)
         row = {}
-        for M in (17, 40, 64, 128, 144, 256, 384, 768):
+        for M in (17, 40, 64, 80, 128, 144, 256, 384, 768):
             x = torch.randn(M, ic, generator=g, device=dev).half()
             y = torch.empty(M, oc, dtype=torch.half, device=dev)
             row[M] = {"fused": t_of(lambda: _native.gemm(x, d["trellis"], d["suh"], d["svh"], K, 0, out=y)),
