@@ -55,6 +55,14 @@ const char* exl3_last_error(void);
 int exl3_abi_version(void);
 
 /*
+ * Capture state of `stream`: *id = 0 when the stream is not being captured into a HIP
+ * graph, else the capture's unique id (hipStreamGetCaptureInfo).  No counterpart in the
+ * reference: the Python layer keys its GEMV workspaces by capture, so that a workspace
+ * whose zero-fill was recorded into one graph is never used outside it.  Host-only.
+ */
+int exl3_stream_capture_id(void* stream, unsigned long long* id);
+
+/*
  * Dense reconstruct: W (ic, oc) fp16 row-major from trellis (ic/16, oc/16, 16K).
  * Replaces ext.reconstruct(W, trellis, K, mcg, mul1)  [orcasaq2/ops.py:56,
  * orcasaq2/__init__.py:57].  W must be 16-byte aligned.  Bit-exact to the format.

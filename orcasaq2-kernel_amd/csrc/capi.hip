@@ -56,7 +56,21 @@ extern "C" {
 
 const char* exl3_last_error(void) { return g_err; }
 
-int exl3_abi_version(void) { return 4; }
+int exl3_abi_version(void) { return 5; }
+
+int exl3_stream_capture_id(void* stream, unsigned long long* id)
+{
+    g_err[0] = 0;
+    if (!id) return set_error(EXL3_ERR_ARG, "exl3_stream_capture_id: null id");
+    *id = 0;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    unsigned long long cid = 0;
+    const hipError_t e = hipStreamGetCaptureInfo(static_cast<hipStream_t>(stream), &st, &cid);
+    if (e != hipSuccess)
+        return set_error(EXL3_ERR_HIP, "exl3_stream_capture_id: %s", hipGetErrorString(e));
+    if (st == hipStreamCaptureStatusActive) *id = cid ? cid : 1;
+    return EXL3_OK;
+}
 
 int exl3_reconstruct(void* W, const void* trellis, int ic, int oc, int K, int codebook, void* stream)
 {

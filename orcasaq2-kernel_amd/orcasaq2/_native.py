@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libexl3hip.so"
 LIB_PATH = os.environ.get("ORCASAQ2_LIB", os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME))
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 CB_3INST, CB_MCG, CB_MUL1 = 0, 1, 2
 GEMV_MAX_ROWS = 16
@@ -36,6 +36,7 @@ class Shard(ctypes.Structure):
 _SIGS = {
     "exl3_last_error": (ctypes.c_char_p, []),
     "exl3_abi_version": (ctypes.c_int, []),
+    "exl3_stream_capture_id": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(ctypes.c_ulonglong)]),
     "exl3_reconstruct": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                         ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "exl3_reconstruct_t": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
@@ -158,24 +159,55 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
+# GEMV workspaces.  A workspace's counter area must be zero when a call starts, and every
+# call that completes leaves it zero again, so one buffer serves every call issued in
+# order on one stream.
+#   _gemv_ws[(device, stream)]            made by an eager call: zero-filled at once.
+#   _gemv_ws_cap[(device, stream, id)]    made inside graph capture `id` because the
+#                                         stream had no large-enough eager workspace: its
+#                                         zero-fill is a node of that graph (run at every
+#                                         replay, before the calls that use it), so it is
+#                                         used by that capture only.
+# A workspace that a captured graph uses is never freed (_gemv_ws_kept): the graph's
+# replays keep writing to it after the eager side has moved on to a larger buffer.
 _gemv_ws: dict = {}
-_gemv_ws_retired: list = []
+_gemv_ws_cap: dict = {}
+_gemv_ws_captured: set = set()
+_gemv_ws_kept: list = []
+
+
+def capture_id(device: torch.device) -> int:
+    """0 when the current stream of `device` is not being captured, else the capture's id."""
+    cid = ctypes.c_ulonglong(0)
+    _check(lib().exl3_stream_capture_id(_stream(device), ctypes.byref(cid)), "exl3_stream_capture_id")
+    return int(cid.value)
 
 
 def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """The GEMV workspace of (device, current stream): zero-filled when created and kept
-    zero in its counter area by every call (exl3hip.h), so it persists across calls and is
-    reused -- also by HIP-graph replays of captured calls.  Calls on one stream run in
-    order, so they can share it; another stream gets its own.  A call needing more gets a
-    larger zeroed buffer; the old one is released in stream order -- except during a graph
-    capture, where nodes already captured still point at it: it is then kept alive for the
-    life of the process."""
+    """The GEMV workspace for a call on the current stream of `device` (see above).  Calls on
+    one stream run in order, so they can share one; another stream gets its own, and so does
+    a graph capture that finds no eager workspace of the size it needs on its stream."""
     stream = torch.cuda.current_stream(device).cuda_stream
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    dev = device.index if device.index is not None else torch.cuda.current_device()
+    key = (dev, stream)
     ws = _gemv_ws.get(key)
+    cid = capture_id(device) if torch.cuda.is_current_stream_capturing() else 0
+    if cid:
+        if ws is None or ws.numel() < nbytes:
+            ckey = (dev, stream, cid)
+            ws = _gemv_ws_cap.get(ckey)
+            if ws is None or ws.numel() < nbytes:
+                if ws is not None:
+                    _gemv_ws_kept.append(ws)
+                ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+                _gemv_ws_cap[ckey] = ws
+                _gemv_ws_kept.append(ws)
+            return ws
+        if ws.data_ptr() not in _gemv_ws_captured:
+            _gemv_ws_captured.add(ws.data_ptr())
+            _gemv_ws_kept.append(ws)
+        return ws
     if ws is None or ws.numel() < nbytes:
-        if ws is not None and torch.cuda.is_current_stream_capturing():
-            _gemv_ws_retired.append(ws)
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _gemv_ws[key] = ws
     return ws

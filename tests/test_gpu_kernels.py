@@ -237,6 +237,21 @@ def test_gemm_rows(native, oracle, rows):
     check_linear_out(y, x, lin, 0, oracle)
 
 
+@pytest.mark.parametrize("rows", [24, 60, 90])
+def test_gemm_single_K_partial_pieces(native, oracle, rows):
+    """Single-shard exl3_gemm on 32-, 64- and 96-row tiles with ic=2048, oc=1024: 4 output
+    tiles of 32 K-steps over 16 workgroups of 8 K-steps, so every tile is split over four
+    workgroups (partial sums through slots, counted arrivals, the last arriver adding the
+    slots in workgroup order).  Repeat calls must be identical."""
+    lin = syn.linear(2048, 1024, 4, seed=rows + 7)
+    x = syn.activations(rows, 2048, torch.Generator().manual_seed(rows + 7))
+    d = to_gpu(lin)
+    y = native.gemm(x.to(dev()), d["trellis"], d["suh"], d["svh"], 4, 0)
+    check_linear_out(y, x, lin, 0, oracle)
+    for _ in range(2):
+        assert torch.equal(native.gemm(x.to(dev()), d["trellis"], d["suh"], d["svh"], 4, 0), y)
+
+
 @pytest.mark.parametrize("K,cb", [(2, 0), (3, 1), (5, 0), (6, 0)])
 def test_gemm_K(native, oracle, K, cb):
     lin = syn.linear(384, 256, K, seed=K)
@@ -261,8 +276,9 @@ def test_gemm_streamk_shapes(native, oracle, rows, ic, oc, K, cb):
 @pytest.mark.parametrize("rows", [1, 5, 17, 40, 64, 80, 100, 200, 450])
 def test_gemm_grouped_mixed_K_and_codebooks(native, oracle, rows):
     """exl3_gemm_grouped: shards of several K (interleaved) and both codebooks that read one
-    A; 64- and 128-row tiles take each codebook's shards in one launch (per-piece K), 256-row
-    tiles one launch per K.  Deterministic across calls."""
+    A; tiles of up to 128 rows (32, 48, 64, 96 or 128 by row count) take each codebook's
+    shards in one launch (per-piece K), 256-row tiles one launch per K.  Deterministic
+    across calls."""
     spec = [(384, 3, 0), (256, 5, 0), (128, 3, 1), (640, 2, 0), (256, 3, 0), (128, 6, 1), (384, 5, 0)]
     x = syn.activations(rows, 768, torch.Generator().manual_seed(50 + rows))
     lins = [syn.linear(768, oc, K, seed=500 + i) for i, (oc, K, _) in enumerate(spec)]

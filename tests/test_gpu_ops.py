@@ -50,40 +50,107 @@ def test_shard_gemm_wrong_width_message(native):
         torch.ops.orcasaq2.shard_gemm(x, lin["trellis"], lin["suh"], lin["svh"], 256, 3.0, False, False)
 
 
-@pytest.mark.parametrize("rows", [1, 2, 9, 40])
-def test_hip_graph_capture_replays(native, oracle, rows):
-    """The op and the grouped op captured into a HIP graph and replayed four times, with
-    eager work between replays, against eager results: 1 row (persistent kernel, its
-    counters rearmed by every call), 2 rows (four-row template), 9 rows (16-row tiles,
-    one launch over both K), 40 rows (prefill: 64-row stream-K tiles, counters zeroed by
-    the set-up kernels inside the graph)."""
-    lins = [syn.linear(1024, oc, K, seed=i) for i, (oc, K) in enumerate([(512, 4), (256, 5)])]
+def _two_shard_step(rows, ic=1024):
+    lins = [syn.linear(ic, oc, K, seed=i) for i, (oc, K) in enumerate([(512, 4), (256, 5)])]
     ds = [on(l) for l in lins]
-    x = syn.activations(rows, 1024, torch.Generator().manual_seed(1)).to(D)
 
-    def step():
+    def step(x):
         a = torch.ops.orcasaq2.shard_gemm(x, ds[0]["trellis"], ds[0]["suh"], ds[0]["svh"], 512, 4.0, False, False)
-        grouped = torch.ops.orcasaq2.shards_gemv if rows <= 16 else torch.ops.orcasaq2.shards_gemm
+        grouped = torch.ops.orcasaq2.shards_gemv if x.shape[0] <= 16 else torch.ops.orcasaq2.shards_gemm
         b = grouped(x, [d["trellis"] for d in ds], [d["suh"] for d in ds], [d["svh"] for d in ds], [512, 256],
                     [4.0, 5.0], [False, False], [False, False])
         return a, b
+    return step
 
-    eager = step()
+
+@pytest.mark.parametrize("rows", [1, 2, 9, 40])
+def test_hip_graph_capture_replays(native, oracle, rows):
+    """The op and the grouped op captured into a HIP graph on a stream that ran them eagerly
+    first (so the capture uses that stream's eager, zero-filled GEMV workspace), replayed four
+    times with eager work between replays, against eager results: 1 row (persistent kernel,
+    its counters rearmed by every call), 2 rows (four-row template), 9 rows (16-row tiles, one
+    launch over both K), 40 rows (prefill: 48-row stream-K tiles, counters zeroed by the
+    set-up kernels inside the graph)."""
+    step = _two_shard_step(rows)
+    x = syn.activations(rows, 1024, torch.Generator().manual_seed(1)).to(D)
+    eager = step(x)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        step()  # warm the per-stream workspace outside capture
-    torch.cuda.current_stream().wait_stream(s)
+        step(x)  # creates this stream's workspace outside the capture
+    torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        out = step()
+    with torch.cuda.graph(g, stream=s):
+        out = step(x)
     for i in range(4):
         x.copy_(syn.activations(rows, 1024, torch.Generator().manual_seed(1)).to(D))
-        g.replay()
+        with torch.cuda.stream(s):
+            g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out[0], eager[0]) and torch.equal(out[1], eager[1]), i
-        step()  # eager work between replays
+        with torch.cuda.stream(s):
+            step(x)  # eager work on the same stream between replays
         torch.cuda.synchronize()
+
+
+def test_graphs_share_workspace_and_survive_its_growth(native):
+    """Two graphs captured on one stream share its eager workspace; an eager 16-row call on
+    that stream then needs a larger workspace (the old one must stay alive for the graphs);
+    the graphs are replayed in reverse capture order, each against eager results."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    steps = {r: _two_shard_step(r) for r in (1, 3)}
+    xs = {r: syn.activations(r, 1024, torch.Generator().manual_seed(10 + r)).to(D) for r in (1, 3)}
+    eager = {r: steps[r](xs[r]) for r in (1, 3)}
+    graphs, outs = {}, {}
+    with torch.cuda.stream(s):
+        steps[1](xs[1])
+        torch.cuda.synchronize()
+        for r in (1, 3):
+            graphs[r] = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graphs[r], stream=s):
+                outs[r] = steps[r](xs[r])
+    torch.cuda.synchronize()
+    x16 = syn.activations(16, 1024, torch.Generator().manual_seed(16)).to(D)
+    with torch.cuda.stream(s):
+        big = _two_shard_step(16)(x16)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for r in (3, 1):
+            with torch.cuda.stream(s):
+                graphs[r].replay()
+            torch.cuda.synchronize()
+            assert torch.equal(outs[r][0], eager[r][0]) and torch.equal(outs[r][1], eager[r][1]), (rep, r)
+        with torch.cuda.stream(s):
+            again = _two_shard_step(16)(x16)
+        torch.cuda.synchronize()
+        assert torch.equal(again[0], big[0]) and torch.equal(again[1], big[1]), rep
+
+
+def test_capture_without_eager_warmup(native):
+    """A capture on a stream that never ran the op eagerly: the workspace is made inside the
+    capture (its zero-fill a node of the graph) and is private to that graph; eager calls on
+    the same stream afterwards get their own, and both stay correct in any order."""
+    step = _two_shard_step(1)
+    x = syn.activations(1, 1024, torch.Generator().manual_seed(21)).to(D)
+    eager = step(x)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out = step(x)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s):
+        e1 = step(x)   # eager before the graph was ever replayed
+    torch.cuda.synchronize()
+    assert torch.equal(e1[0], eager[0]) and torch.equal(e1[1], eager[1])
+    for i in range(3):
+        with torch.cuda.stream(s):
+            g.replay()
+            e2 = step(x)
+        torch.cuda.synchronize()
+        assert torch.equal(out[0], eager[0]) and torch.equal(out[1], eager[1]), i
+        assert torch.equal(e2[0], eager[0]) and torch.equal(e2[1], eager[1]), i
 
 
 def test_torch_compile_treats_op_as_opaque(native):
@@ -162,3 +229,23 @@ def test_reconstruct_weight_dense_equivalence(native, oracle):
     y = torch.ops.orcasaq2.shard_gemm(x, d["trellis"], d["suh"], d["svh"], 384, 4.0, False, False)
     err = torch.linalg.norm(y.float() - y_dense, dim=1) / torch.linalg.norm(y_dense, dim=1)
     assert err.max().item() < 2e-3
+
+
+def test_reconstruct_weight_matches_oracle_deploy_weight(native, oracle):
+    """reconstruct_weight (HIP W_q + fp32 Hadamard/sign algebra, orcasaq2/__init__.py:49-61)
+    against the oracle's fp64 deploy weight on the oracle's own W_q: every element within
+    half an fp16 ulp of the fp64 value plus the fp32 algebra's absolute rounding (two
+    128-term Hadamard sums: at most ~2^-18 of the largest element; 2^-16 allowed), so a
+    wrong sign, index or transposition -- an error of the order of the elements -- fails."""
+    from orcasaq2 import reconstruct_weight
+    for K, cb, (ic, oc) in ((4, 0, (256, 384)), (3, 1, (384, 128)), (5, 0, (5120, 1024))):
+        lin = syn.linear(ic, oc, K, seed=40 + K)
+        d = on(lin)
+        mcg = torch.ones(1, device=D) if cb else None
+        W = reconstruct_weight(d["trellis"], d["suh"], d["svh"], mcg, None).cpu().numpy().astype(np.float64)
+        ref = oracle.deploy_weight(oracle.reconstruct_f16(lin["trellis"], K, cb), lin["suh"].numpy(),
+                                   lin["svh"].numpy())
+        assert W.shape == ref.shape == (oc, ic)
+        ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+        bound = 0.5 * ulp + 2.0 ** -16 * np.abs(ref).max()
+        assert (np.abs(W - ref) <= bound).all(), (K, cb, np.max(np.abs(W - ref) / bound))
