@@ -125,6 +125,21 @@ int exl3_gemv_grouped(const void* A, const exl3_shard_t* shards, int nshards, vo
                       size_t ws_bytes, int rows, int ic, void* stream);
 
 /*
+ * exl3_gemv_grouped without a workspace argument: it allocates nothing (no hipMalloc, no
+ * library allocation), for callers that cannot allocate -- code under HIP-graph capture,
+ * serving loops that forbid device allocation.  No counterpart in the reference.
+ * The scratch is a file-scope device array of EXL3_STATIC_SCRATCH_BYTES (16 MiB), one per
+ * GPU, held until the process ends; a call whose exl3_gemv_grouped_workspace_bytes exceeds
+ * it fails with EXL3_ERR_WORKSPACE (rows 1..4 fit every shape of the 27B model and its
+ * 151936-wide lm_head; rows 5..16 fit single 5120-output shards).  All calls on one GPU
+ * share the array and each leaves it ready for the next, so calls issued in order (one
+ * stream, or graph replays in order) are safe; calls that may overlap in time race on it.
+ */
+#define EXL3_STATIC_SCRATCH_BYTES (16u << 20)
+int exl3_gemv_grouped_static(const void* A, const exl3_shard_t* shards, int nshards, int rows, int ic,
+                             void* stream);
+
+/*
  * Prefill GEMM, any rows >= 1 (meant for rows > 16): same result as exl3_gemv, computed
  * as one Hadamard pass over A into the workspace plus one kernel that decodes trellis
  * tiles into fp16 MFMA operands (no dense W_q in HBM) and applies H and svh on output.

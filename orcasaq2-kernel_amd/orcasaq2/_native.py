@@ -52,6 +52,8 @@ _SIGS = {
     "exl3_gemv_grouped": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Shard), ctypes.c_int,
                                          ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
                                          ctypes.c_void_p]),
+    "exl3_gemv_grouped_static": (ctypes.c_int, [ctypes.c_void_p, ctypes.POINTER(Shard), ctypes.c_int,
+                                                ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
     "exl3_gemm_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
     "exl3_gemm": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
