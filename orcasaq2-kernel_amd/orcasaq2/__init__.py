@@ -14,6 +14,9 @@ kernels behind a C ABI (include/exl3hip.h) -- instead of the exllamav3 CUDA exte
     whose loader captures each shard.
 Tensor parallelism is not implemented; TP > 1 raises rather than serving wrong numbers.
 """
+import functools
+import inspect
+
 import torch
 
 from . import _native
@@ -57,13 +60,10 @@ def reconstruct_weight(trellis, suh, svh, mcg, mul1):
     return w.t().contiguous().half()
 
 
-def register():
-    """vLLM general-plugin entry point (orcasaq2/__init__.py:64-94): fail fast if the HIP
-    library cannot be loaded, register quant_method "exl3" (idempotent), and wrap the
-    embedding / lm_head constructors."""
-    from ._vllm_compat import init_logger, register_quantization_config
-
-    logger = init_logger("vllm.orcasaq2")
+def _require_library() -> None:
+    """Fail at plugin registration, not in the middle of a forward pass, when the HIP
+    library cannot be loaded (the reference fails there on a missing exllamav3 wheel,
+    orcasaq2/__init__.py:74-85)."""
     try:
         _native.lib()
     except Exception as e:
@@ -75,57 +75,78 @@ def register():
             "on a ROCm 7 machine (hipcc --offload-arch=gfx950)."
         ) from e
 
+
+def register():
+    """vLLM general-plugin entry point (reference orcasaq2/__init__.py:64-94): check the HIP
+    library, register quant_method "exl3", and let embed_tokens / lm_head see the EXL3
+    config.  A second call in the same process changes nothing."""
+    from ._vllm_compat import init_logger, register_quantization_config
     from .config import Exl3Config
 
+    logger = init_logger("vllm.orcasaq2")
+    _require_library()
     try:
         register_quantization_config("exl3")(Exl3Config)
-    except ValueError:
-        return  # already registered in this process
-    _patch_embedding_layers(logger)
-    logger.info("orcasaq2 armed: quant_method 'exl3' is now loadable")
+    except ValueError:   # vLLM refuses a name twice: this process is armed already
+        return
+    wrapped = _patch_embedding_layers(logger)
+    logger.info("orcasaq2 armed: quant_method 'exl3' is now loadable (%s wrapped)", ", ".join(wrapped) or "nothing")
 
 
-def _patch_embedding_layers(logger):
-    """Give VocabParallelEmbedding and ParallelLMHead the quant config that model files
-    construct them without (orcasaq2/__init__.py:97-153).  Each constructor is wrapped; the
-    wrapper binds the call against the real signature and fills `quant_config` only when it
-    is empty and the current vLLM config is an Exl3Config.  Idempotent."""
-    import inspect
-
+def _current_exl3_config():
+    """The current vLLM config's quant config when it is an Exl3Config, else None."""
     from . import _vllm_compat as vc
     from .config import Exl3Config
 
-    if getattr(vc.VocabParallelEmbedding, "_orca_patched", False):
-        return
+    try:
+        cfg = vc.get_current_vllm_config()
+    except Exception:
+        return None
+    for holder in (cfg, getattr(cfg, "model_config", None)):
+        qc = getattr(holder, "quant_config", None)
+        if qc is not None:
+            return qc if isinstance(qc, Exl3Config) else None
+    return None
 
-    def _current_exl3_config():
-        try:
-            cfg = vc.get_current_vllm_config()
-        except Exception:
-            return None
-        qc = getattr(cfg, "quant_config", None) or \
-            getattr(getattr(cfg, "model_config", None), "quant_config", None)
-        return qc if isinstance(qc, Exl3Config) else None
 
-    for cls in (vc.VocabParallelEmbedding, vc.ParallelLMHead):
-        def make(orig_init):
-            sig = inspect.signature(orig_init)
+def _wrap_constructor(cls) -> bool:
+    """Wraps cls.__init__ (once per class) so that a call which leaves `quant_config` empty
+    gets the current EXL3 config.  The argument is found by its position in the
+    constructor's signature: vLLM's ParallelLMHead hands it to its (also wrapped) parent
+    positionally, model code usually omits it.  Returns False when there is nothing to do."""
+    if cls.__dict__.get("_orca_patched"):
+        return False
+    orig = cls.__init__
+    names = list(inspect.signature(orig).parameters)
+    if "quant_config" not in names:
+        return False
+    at = names.index("quant_config")          # position counting `self`
 
-            def __init__(self, *args, **kwargs):
-                # ParallelLMHead passes quant_config to its (also wrapped) parent
-                # positionally, so bind against the signature instead of adding a keyword.
-                try:
-                    bound = sig.bind_partial(self, *args, **kwargs)
-                except TypeError:
-                    return orig_init(self, *args, **kwargs)
-                if bound.arguments.get("quant_config") is None:
-                    qc = _current_exl3_config()
-                    if qc is not None:
-                        bound.arguments["quant_config"] = qc
-                        return orig_init(*bound.args, **bound.kwargs)
-                return orig_init(self, *args, **kwargs)
-            return __init__
+    @functools.wraps(orig)
+    def __init__(self, *args, **kwargs):
+        positional = len(args) >= at
+        if (args[at - 1] if positional else kwargs.get("quant_config")) is None:
+            qc = _current_exl3_config()
+            if qc is not None:
+                if positional:
+                    args = args[:at - 1] + (qc,) + args[at:]
+                else:
+                    kwargs["quant_config"] = qc
+        orig(self, *args, **kwargs)
 
-        cls.__init__ = make(cls.__init__)
-    vc.VocabParallelEmbedding._orca_patched = True
-    logger.info("orcasaq2: embed_tokens / lm_head will receive the EXL3 quant config")
+    cls.__init__ = __init__
+    cls._orca_patched = True
+    return True
+
+
+def _patch_embedding_layers(logger) -> list[str]:
+    """Model files build embed_tokens and lm_head without a quant config, so vLLM would never
+    ask this plugin about them; wrap both constructors to supply the current EXL3 config
+    when it was left out (reference orcasaq2/__init__.py:97-153).  Layers of other quant
+    methods are untouched."""
+    from . import _vllm_compat as vc
+
+    wrapped = [cls.__name__ for cls in (vc.VocabParallelEmbedding, vc.ParallelLMHead) if _wrap_constructor(cls)]
+    if wrapped:
+        logger.info("orcasaq2: %s receive the EXL3 quant config", " and ".join(wrapped))
+    return wrapped

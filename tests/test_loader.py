@@ -121,11 +121,11 @@ def test_read_config_and_plan(pack_dir):
 
 def _check_structure(mods):
     qkv = mods["model.layers.0.self_attn.qkv_proj"]
-    assert [(s["K"], s["ic"], s["oc"], s["mcg"]) for s in qkv.exl3_shards] == \
+    assert [(s.K, s.ic, s.oc, s.mcg) for s in qkv.exl3_shards] == \
         [(4, H, H, False), (5, H, KV, False), (5, H, KV, False)]
     gu = mods["model.layers.0.mlp.gate_up_proj"]
-    assert [(s["K"], s["oc"], s["mcg"], s["mul1"]) for s in gu.exl3_shards] == [(3, I, True, False)] * 2
-    assert mods["model.layers.1.mlp.gate_up_proj"].exl3_shards[1]["K"] == 2
+    assert [(s.K, s.oc, s.mcg, s.mul1) for s in gu.exl3_shards] == [(3, I, True, False)] * 2
+    assert mods["model.layers.1.mlp.gate_up_proj"].exl3_shards[1].K == 2
     d1 = mods["model.layers.1.self_attn.qkv_proj"]
     assert d1.exl3_shards is None and tuple(d1.exl3_dense.shape) == (H + 2 * KV, H)
     o1 = mods["model.layers.1.self_attn.o_proj"]
@@ -133,7 +133,7 @@ def _check_structure(mods):
     emb = mods["model.embed_tokens"]
     assert emb.exl3_embed_q.dtype == torch.int8 and tuple(emb.exl3_embed_s.shape) == (V, 1)
     head = mods["lm_head"]
-    assert head.exl3_shards[0]["K"] == 6 and head.exl3_shards[0]["oc"] == V
+    assert head.exl3_shards[0].K == 6 and head.exl3_shards[0].oc == V
     for m in mods.values():
         for p in ("trellis", "suh", "svh", "qweight"):
             assert not hasattr(m, p), "placeholders are dropped after loading"
@@ -149,7 +149,7 @@ def test_load_sharded_pack_and_config_json(tmp_path):
     _check_structure(mods)
     a = loader.load(str(tmp_path), device="cpu", only=["model.layers.0.mlp.down_proj"])
     assert list(a) == ["model.layers.0.mlp.down_proj"]
-    assert torch.equal(a["model.layers.0.mlp.down_proj"].exl3_shards[0]["trellis"].cpu(),
+    assert torch.equal(a["model.layers.0.mlp.down_proj"].exl3_shards[0].trellis.cpu(),
                        _mods()["model.layers.0.mlp.down_proj"]["trellis"])
 
 
@@ -195,7 +195,7 @@ def test_loaded_modules_match_oracle(pack_dir, oracle, native, rows):
     for key, m in mods.items():
         if m.kind == "embedding":
             continue
-        ic = (m.exl3_shards[0]["ic"] if m.exl3_shards is not None else m.exl3_dense.shape[1])
+        ic = (m.exl3_shards[0].ic if m.exl3_shards is not None else m.exl3_dense.shape[1])
         x = syn.activations(rows, ic, g)
         y = m(x.cuda()).float().cpu().numpy()
         col = 0

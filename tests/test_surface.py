@@ -98,9 +98,9 @@ def test_fused_layer_apply_matches_oracle(cpu_ops, oracle):
     _load(layer, lins, ["k", "v", "q"])
     layer.quant_method.process_weights_after_loading(layer)
     assert not hasattr(layer, "trellis") and layer.exl3_dense is None
-    assert [s["oc"] for s in layer.exl3_shards] == [256, 128, 128]
-    assert [s["K"] for s in layer.exl3_shards] == [4, 5, 5]
-    assert all(s["suh"].dtype == torch.half for s in layer.exl3_shards)
+    assert [s.oc for s in layer.exl3_shards] == [256, 128, 128]
+    assert [s.K for s in layer.exl3_shards] == [4, 5, 5]
+    assert all(s.suh.dtype == torch.half for s in layer.exl3_shards)
     layer.bias.data = torch.randn(512)
     # grouped decode-GEMV to 16 rows, grouped GEMM to GEMM_MAX_ROWS (144), per shard above
     route = {1: ["shards_gemv"], 3: ["shards_gemv"], 20: ["shards_gemm"], 144: ["shards_gemm"],
@@ -137,6 +137,23 @@ def test_load_errors():
     layer = vc.LinearBase(128, 128, quant_config=cfg, prefix="p")
     with pytest.raises(RuntimeError, match="no trellis and no dense weight"):
         layer.quant_method.process_weights_after_loading(layer)
+
+    layer = vc.LinearBase(128, 128, quant_config=cfg, prefix="p")
+    layer.trellis.weight_loader(layer.trellis, lin["trellis"], None)
+    layer.suh.weight_loader(layer.suh, lin["suh"], None)
+    with pytest.raises(RuntimeError, match="trellis shard 0 arrived without its suh/svh"):
+        layer.quant_method.process_weights_after_loading(layer)
+
+
+def test_newer_loader_hooks_file_by_slot():
+    """vLLM's BasevLLMParameter hooks (load_qkv_weight & co.) file the tensor like
+    weight_loader does, with the shard id under either keyword."""
+    p = Exl3ShardParam(suffix="suh")
+    a, b = torch.ones(4), torch.zeros(4)
+    p.load_qkv_weight(a, shard_id="v")
+    p.load_merged_column_weight(b, loaded_shard_id=1)
+    p.load_row_parallel_weight(b)
+    assert p.shards[2] is a and p.shards[1] is b and p.shards[0] is b
 
 
 def test_dense_fallback_layer():
