@@ -257,13 +257,21 @@ def prefill_bench(reps: int) -> dict:
     return out
 
 
+CODEBOOK_RMS = 1.2437   # RMS of the 3INST codebook's 2^16 values
+
+
 def stack_bench(tokens: int = 20) -> dict:
     """Config 4: the linear stack of a 64-layer Qwen-27B-shaped decoder at batch-1 decode,
     one token = the int8 embedding gather, per layer the grouped q/k/v GEMV, o_proj, the
     grouped gate/up GEMV and down_proj (K from the seeded {2,3,4,5} draw), then the K=6
-    lm_head.  Attention, norms and the activation function are excluded (BASELINE
-    config 4); each projection reads a fixed activation of its input width, which changes
-    no work.  The token is captured once into a HIP graph and replayed `tokens` times."""
+    lm_head.  Attention, norms, residuals and the activation function are excluded
+    but every projection reads what the one before it produced, so
+    nothing runs before its input exists: o_proj reads the q columns of qkv (the width of
+    the attention output it stands for), gate/up read o_proj's output, down_proj reads the
+    gate columns, the next layer reads down_proj's output, the lm_head the last one.  The
+    svh scales are |N(0,1)|/sqrt(ic)/CODEBOOK_RMS so each projection keeps the activation
+    RMS and 257 chained projections stay finite in fp16.  The token is captured once into
+    a HIP graph and replayed `tokens` times."""
     import torch
     from orcasaq2 import _native
     from orcasaq2 import synthetic as syn
@@ -273,41 +281,50 @@ def stack_bench(tokens: int = 20) -> dict:
     shapes = syn.stack_shapes()
     layers = []
     nbytes = 0
+
+    def lin(ic, oc, K):
+        d = _rand_linear(ic, oc, K, g, dev)
+        d["svh"] = (d["svh"].float() / CODEBOOK_RMS).half()
+        return d
+
     for bits in syn.stack_bits():
-        L = {n: _rand_linear(*shapes[n], bits[n], g, dev) for n in shapes}
+        layers.append({n: lin(*shapes[n], bits[n]) for n in shapes})
         nbytes += sum(syn.packed_bytes(*shapes[n], bits[n]) for n in shapes)
-        layers.append(L)
-    head = _rand_linear(syn.HIDDEN, syn.VOCAB, 6, g, dev)
+    head = lin(syn.HIDDEN, syn.VOCAB, 6)
     nbytes += syn.packed_bytes(syn.HIDDEN, syn.VOCAB, 6)
     table = torch.randint(-128, 128, (syn.VOCAB, syn.HIDDEN), generator=g, device=dev, dtype=torch.int8)
-    scales = (torch.rand(syn.VOCAB, 1, generator=g, device=dev) * 0.02).half()
+    scales = (torch.rand(syn.VOCAB, 1, generator=g, device=dev) * 0.02 + 0.001).half()
     ids = torch.tensor([12345], device=dev)
     nbytes += syn.HIDDEN + 2
-    xh = torch.randn(1, syn.HIDDEN, generator=g, device=dev).half()
-    xq = torch.randn(1, syn.Q_OUT, generator=g, device=dev).half()
-    xi = torch.randn(1, syn.INTERMEDIATE, generator=g, device=dev).half()
     y_qkv = torch.empty(1, syn.Q_OUT + 2 * syn.KV_OUT, dtype=torch.half, device=dev)
+    y_o = torch.empty(1, syn.HIDDEN, dtype=torch.half, device=dev)
     y_gu = torch.empty(1, 2 * syn.INTERMEDIATE, dtype=torch.half, device=dev)
     y_h = torch.empty(1, syn.HIDDEN, dtype=torch.half, device=dev)
     logits = torch.empty(1, syn.VOCAB, dtype=torch.half, device=dev)
+    q_cols = y_qkv[:, :syn.Q_OUT]           # one row: a contiguous view
+    gate_cols = y_gu[:, :syn.INTERMEDIATE]
 
     def token():
-        _native.embed_int8(table, scales, ids)
+        h = _native.embed_int8(table, scales, ids)
         for L in layers:
-            _native.gemv_grouped(xh, [L["q"], L["k"], L["v"]], out=y_qkv)
-            _native.gemv_grouped(xq, [L["o"]], out=y_h)
-            _native.gemv_grouped(xh, [L["gate"], L["up"]], out=y_gu)
-            _native.gemv_grouped(xi, [L["down"]], out=y_h)
-        _native.gemv_grouped(xh, [head], out=logits)
+            _native.gemv_grouped(h, [L["q"], L["k"], L["v"]], out=y_qkv)
+            _native.gemv_grouped(q_cols, [L["o"]], out=y_o)
+            _native.gemv_grouped(y_o, [L["gate"], L["up"]], out=y_gu)
+            _native.gemv_grouped(gate_cols, [L["down"]], out=y_h)
+            h = y_h
+        _native.gemv_grouped(h, [head], out=logits)
 
     graph, side = _graph(dev, token)
     sec = _time_graph(graph, side, tokens)
+    finite = bool(torch.isfinite(logits).all().item())
+    rms = float(logits.float().pow(2).mean().sqrt().item())
     del graph
     return {"tok_s": round(1.0 / sec, 2), "ms_per_token": round(sec * 1e3, 4), "bytes_per_token": nbytes,
             "GB/s": round(nbytes / sec / 1e9, 1), "frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
-            "tokens": tokens,
+            "tokens": tokens, "logits_finite": finite, "logits_rms": round(rms, 4),
             "what": "config4 measured: 64-layer Qwen-27B-shaped linear stack + K=6 lm_head + int8 embedding "
-                    "gather, batch 1, one HIP-graph-launched token replayed; attention/KV excluded"}
+                    "gather, batch 1, each projection chained on the previous output, one HIP-graph-launched "
+                    "token replayed; attention/KV/norms/activation excluded"}
 
 
 def config2_bench(reps: int) -> dict:
@@ -413,56 +430,107 @@ def config3_bench(reps: int) -> dict:
                               "frac": round(rbytes / t_rect / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
-def cpu_baseline(max_seconds: float = 30.0) -> dict:
-    """The reference's CPU path on one step of the workload (K = 2, 3, 4, 5 GEMVs):
-    oracle trellis decode -> reconstruct_weight's fp32 Hadamard/sign algebra
-    (orcasaq2/__init__.py:58-61) -> F.linear (orcasaq2/config.py:230)."""
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(runs: int = 5) -> dict:
+    """The reference's CPU path, timed on this host (median of `runs` after one warm-up run):
+
+    * value (all os.cpu_count() threads): oracle trellis decode -> reconstruct_weight's fp32
+      Hadamard/sign algebra (reference orcasaq2/__init__.py:49-61) -> F.linear
+      (orcasaq2/config.py:230), one batch-1 GEMV at each K = 2, 3, 4, 5 of down_proj
+      (17408 -> 5120) restricted to its first 512 output columns (a bounded sample; the
+      rate is per packed byte, so it does not depend on the column count);
+    * the same path on one thread (first 128 columns);
+    * the activation-side ordering of the same math (orcasaq2/ops.py:53-59: H(x*suh), the
+      decoded W_q, H(y)*svh) on all threads;
+    * config 0: the full 5120 -> 5120 K=4 layer, batch 1, the reference ordering, all threads.
+    """
     import torch
     from oracle import oracle as O
     from orcasaq2 import _t128
     from orcasaq2 import synthetic as syn
 
-    # this host's share of cores for one GPU (the GPU boxes grant 16 per GPU)
-    threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
-    ic, oc = syn.INTERMEDIATE, syn.HIDDEN
-    x = syn.activations(1, ic, torch.Generator().manual_seed(11))
-    t_dec = t_had = t_mm = 0.0
-    nbytes = 0
-    t_start = time.perf_counter()
-    for K in (2, 3, 4, 5):
-        lin = syn.linear(ic, oc, K, seed=K)
+    threads = os.cpu_count() or 1
+    x17 = syn.activations(1, syn.INTERMEDIATE, torch.Generator().manual_seed(11))
+
+    def sample(ic, oc_cols, K, seed):
+        lin = syn.linear(ic, syn.HIDDEN, K, seed=seed)
+        return dict(trellis=lin["trellis"][:, :oc_cols // 16].contiguous(), suh=lin["suh"],
+                    svh=lin["svh"][:oc_cols].contiguous(), K=K, ic=ic, oc=oc_cols)
+
+    def weight_side(x, d, nthreads):
+        """decode, H.W_q.H algebra on the weight, then the product; seconds per phase."""
         a = time.perf_counter()
-        wq = torch.from_numpy(O.reconstruct_f16(lin["trellis"], K, 0, nthreads=threads))
+        wq = torch.from_numpy(O.reconstruct_f16(d["trellis"], d["K"], 0, nthreads=nthreads))
         b = time.perf_counter()
         w = wq.float()
-        w = _t128(w.t()).t() * lin["suh"].float().unsqueeze(1)
-        w = _t128(w) * lin["svh"].float().unsqueeze(0)
+        w = _t128(w.t()).t() * d["suh"].float().unsqueeze(1)
+        w = _t128(w) * d["svh"].float().unsqueeze(0)
         w = w.t().contiguous().half()
         c = time.perf_counter()
         y = torch.nn.functional.linear(x, w)
-        d = time.perf_counter()
-        assert y.shape == (1, oc)
-        t_dec += b - a
-        t_had += c - b
-        t_mm += d - c
-        nbytes += syn.packed_bytes(ic, oc, K)
-        if time.perf_counter() - t_start > max_seconds:
-            break
-    total = t_dec + t_had + t_mm
-    cpu = "unknown"
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": nbytes / total / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"one step of the workload ({nbytes / 1e6:.1f} MB packed: down_proj at "
-                      "K=2,3,4,5): oracle C decode (OpenMP) + fp32 torch Hadamard algebra + "
-                      f"fp16 F.linear; decode {t_dec:.2f}s, hadamard {t_had:.2f}s, "
-                      f"matmul {t_mm:.2f}s; CPU: {cpu}"}
+        e = time.perf_counter()
+        assert y.shape == (1, d["oc"])
+        return b - a, c - b, e - c
+
+    def act_side(x, d, nthreads):
+        a = time.perf_counter()
+        wq = torch.from_numpy(O.reconstruct_f16(d["trellis"], d["K"], 0, nthreads=nthreads))
+        b = time.perf_counter()
+        xh = _t128(x.float() * d["suh"].float()).half()
+        y = (xh.float() @ wq.float()).half()
+        y = (_t128(y.float()) * d["svh"].float()).half()
+        c = time.perf_counter()
+        assert y.shape == (1, d["oc"])
+        return b - a, c - b, 0.0
+
+    def median_rate(fn, ds, x, nthreads):
+        torch.set_num_threads(nthreads)
+        nbytes = sum(syn.packed_bytes(d["ic"], d["oc"], d["K"]) for d in ds)
+        for d in ds:                          # warm-up run
+            fn(x, d, nthreads)
+        totals, phases = [], []
+        for _ in range(runs):
+            p = [fn(x, d, nthreads) for d in ds]
+            phases.append([sum(v[i] for v in p) for i in range(3)])
+            totals.append(sum(phases[-1]))
+        med = statistics.median(totals)
+        ph = phases[totals.index(sorted(totals)[len(totals) // 2])]
+        return nbytes / med / 1e9, med, ph, nbytes
+
+    wide = [sample(syn.INTERMEDIATE, 512, K, seed=K) for K in (2, 3, 4, 5)]
+    narrow = [dict(d, trellis=d["trellis"][:, :8].contiguous(), svh=d["svh"][:128].contiguous(), oc=128)
+              for d in wide]
+    v_all, t_all, ph_all, nb_all = median_rate(weight_side, wide, x17, threads)
+    v_one, t_one, ph_one, nb_one = median_rate(weight_side, narrow, x17, 1)
+    v_act, t_act, ph_act, _ = median_rate(act_side, wide, x17, threads)
+    c0 = syn.linear(syn.HIDDEN, syn.HIDDEN, 4, seed=0)
+    c0 = dict(c0, K=4)
+    x0 = syn.activations(1, syn.HIDDEN, torch.Generator().manual_seed(0))
+    v_c0, t_c0, _, nb_c0 = median_rate(weight_side, [c0], x0, threads)
+    return {"value": round(v_all, 5), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"reference CPU path (oracle C decode + reconstruct_weight fp32 Hadamard algebra + "
+                      f"F.linear), one batch-1 GEMV at each K=2,3,4,5 of down_proj 17408->5120 restricted "
+                      f"to its first 512 outputs ({nb_all / 1e6:.1f} MB packed), median of {runs} runs on "
+                      f"{threads} threads: {t_all:.2f} s per run (decode {ph_all[0]:.2f}, hadamard "
+                      f"{ph_all[1]:.2f}, matmul {ph_all[2]:.3f}); CPU: {_cpu_model()}",
+            "one_thread": {"value": round(v_one, 5), "unit": "GB/s", "s_per_run": round(t_one, 3),
+                           "sample": f"same path, first 128 outputs ({nb_one / 1e6:.2f} MB packed), 1 thread"},
+            "activation_side": {"value": round(v_act, 5), "unit": "GB/s", "s_per_run": round(t_act, 3),
+                                "sample": "orcasaq2/ops.py:53-59 ordering (H(x*suh), decoded W_q, "
+                                          f"H(y)*svh), same sample, {threads} threads; decode "
+                                          f"{ph_act[0]:.2f} s, rest {ph_act[1]:.3f} s"},
+            "config0": {"value": round(v_c0, 5), "unit": "GB/s", "s_per_run": round(t_c0, 3),
+                        "sample": f"5120->5120 K=4 batch 1 ({nb_c0 / 1e6:.1f} MB packed), reference ordering, "
+                                  f"{threads} threads"}}
 
 
 def main():
