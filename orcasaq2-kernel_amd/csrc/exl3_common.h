@@ -213,41 +213,44 @@ __device__ __forceinline__ f16x8 chunk_hfragment(const uint32_t (&w)[K + 1], con
 
 // ---------------------------------------------------------------- codebook (batch-1 dot2 form)
 //
-// 3INST in offset form: a = 89226354 and b = 64248484 are both even, so with
-// C = (b/2) * (a/2)^-1 mod 2^31 = 0x68b437e2,  a*s + b = a*(s + C) (mod 2^32) for every
-// 16-bit state s.  One SDWA add then both takes the state out of the low or high half of
-// a 32-bit register and adds C, and one v_mul_lo_u32 finishes x -- two VALU ops where the
-// clean-shift / multiply / add form needs three.  MCG (b = 0) multiplies the clean state.
+// Three VALU ops per position, whatever K is:
+//  * a state on a 16-bit boundary of a word (the low or high half): 3INST in offset form --
+//    a = 89226354 and b = 64248484 are both even, so with C = (b/2) * (a/2)^-1 mod 2^31 =
+//    0x68b437e2, a*s + b = a*(s + C) (mod 2^32) for every 16-bit state s; one SDWA add takes
+//    the half out and adds C, one v_mul_lo_u32 finishes x.  MCG (b = 0): a shift or mask,
+//    then the multiply.
+//  * any other state: one v_bfe_u32 takes the clean 16-bit field (out of the word, or out of
+//    the 32 bits centred on a word boundary when it straddles one -- one v_alignbit per
+//    boundary, shared by every state across it), and one v_mad_u64_u32 forms a*s + b (its
+//    low half; measured on MI355X at the rate of v_mul_lo_u32).
+// Then one v_bitop3_b32 masks the word.
 constexpr uint32_t CB3_OFFSET = 0x68b437e2u;
+constexpr uint32_t CB3_MUL = 89226354u;
+constexpr uint32_t CB3_ADD = 64248484u;
+constexpr uint32_t CBMCG_MUL = 0xCBAC1FEDu;
 
 // Where chunk position Q's 16-bit state is taken from.  E = stream end bit (exclusive) of
 // the state inside w[0]:w[1]:..:w[K] (MSB first), word wi = (E-1)/32, r = E%32:
 //   0: low half of w[wi] (r = 0)            1: high half of w[wi] (r = 16)
-//   2: low half of the window ending at E    (straddles a word boundary; K | 16)
-//   3: high half of the window ending at E+16 (inside w[wi]; K | 16; that window is the
-//      kind-2 window of position Q + 16/K, so the two share one v_alignbit)
-//   4: low half of w[wi] >> (32 - r)          (inside w[wi])
-//   5: low half of W16 >> (16 - r), W16 = the 32 bits centred on the boundary before
-//      w[wi] (straddles; K not dividing 16: one v_alignbit per boundary)
+//   2: bits [32 - r, 48 - r) of w[wi] (r > 16: inside the word)
+//   3: bits [16 - r, 32 - r) of W16, the 32 bits centred on the boundary before w[wi]
+//      (0 < r < 16: the state straddles that boundary)
 template <int K, int Q>
 struct StatePlan {
     static constexpr int E = 32 + (Q + 1) * K;
     static constexpr int wi = (E - 1) >> 5;
     static constexpr int r = E & 31;
-    static constexpr bool pairs = (16 % K) == 0;
-    static constexpr int kind = r == 0 ? 0 : r == 16 ? 1
-        : (r < 16 ? (pairs ? 2 : 5) : ((pairs && E + 16 <= 32 * (K + 1)) ? 3 : 4));
+    static constexpr int kind = r == 0 ? 0 : r == 16 ? 1 : r > 16 ? 2 : 3;
 };
 
+// Clean 16-bit state of a kind-2 or kind-3 position (one v_bfe_u32).
 template <int K, int Q>
-__device__ __forceinline__ uint32_t state_src(const uint32_t (&w)[K + 1])
+__device__ __forceinline__ uint32_t state_field(const uint32_t (&w)[K + 1])
 {
     using P = StatePlan<K, Q>;
-    if constexpr (P::kind == 0 || P::kind == 1) return w[P::wi];
-    else if constexpr (P::kind == 2) return window<K, P::E>(w);
-    else if constexpr (P::kind == 3) return window<K, P::E + 16>(w);
-    else if constexpr (P::kind == 4) return w[P::wi] >> (32 - P::r);
-    else return window<K, 32 * P::wi + 16>(w) >> (16 - P::r);
+    static_assert(P::kind >= 2, "aligned states are read as halves");
+    if constexpr (P::kind == 2) return (w[P::wi] >> (32 - P::r)) & 0xffffu;
+    else return (window<K, 32 * P::wi + 16>(w) >> (16 - P::r)) & 0xffffu;
 }
 
 __device__ __forceinline__ uint32_t sdwa_add_lo(uint32_t v, uint32_t c)
@@ -266,8 +269,16 @@ __device__ __forceinline__ uint32_t sdwa_add_hi(uint32_t v, uint32_t c)
     return d;
 }
 
+// Low half of s * m + b (one v_mad_u64_u32; the carry-out goes to vcc, declared clobbered).
+__device__ __forceinline__ uint32_t mad_lo(uint32_t s, uint32_t m, uint64_t b)
+{
+    uint64_t d;
+    asm("v_mad_u64_u32 %0, vcc, %1, %2, %3" : "=v"(d) : "v"(s), "v"(m), "s"(b) : "vcc");
+    return (uint32_t)d;
+}
+
 struct Dot2Consts {
-    uint32_t mask, flip, off;   // 0x8FFF8FFF, 0x3B603B60, CB3_OFFSET pinned in VGPRs
+    uint32_t mask, flip, off, mul;   // 0x8FFF8FFF, 0x3B603B60, CB3_OFFSET, CB3_MUL pinned in VGPRs
 };
 
 __device__ __forceinline__ Dot2Consts dot2_consts()
@@ -276,6 +287,7 @@ __device__ __forceinline__ Dot2Consts dot2_consts()
     asm volatile("v_mov_b32 %0, 0x8fff8fff" : "=v"(k.mask));
     asm volatile("v_mov_b32 %0, 0x3b603b60" : "=v"(k.flip));
     asm volatile("v_mov_b32 %0, 0x68b437e2" : "=v"(k.off));
+    asm volatile("v_mov_b32 %0, %1" : "=v"(k.mul) : "i"(CB3_MUL));
     return k;
 }
 
@@ -284,14 +296,17 @@ template <int K, int CB, int Q>
 __device__ __forceinline__ uint32_t dot2_word(const uint32_t (&w)[K + 1], const Dot2Consts& k)
 {
     using P = StatePlan<K, Q>;
-    const uint32_t src = state_src<K, Q>(w);
     uint32_t x;
-    if constexpr (CB == CB_MCG) {
-        const uint32_t s = (P::kind == 1 || P::kind == 3) ? (src >> 16) : (src & 0xffffu);
-        x = s * 0xCBAC1FEDu;
+    if constexpr (P::kind <= 1) {
+        const uint32_t src = w[P::wi];
+        if constexpr (CB == CB_MCG) {
+            x = (P::kind == 1 ? (src >> 16) : (src & 0xffffu)) * CBMCG_MUL;
+        } else {
+            x = (P::kind == 1 ? sdwa_add_hi(src, k.off) : sdwa_add_lo(src, k.off)) * CB3_MUL;
+        }
     } else {
-        const uint32_t s = (P::kind == 1 || P::kind == 3) ? sdwa_add_hi(src, k.off) : sdwa_add_lo(src, k.off);
-        x = s * 89226354u;
+        const uint32_t s = state_field<K, Q>(w);
+        x = CB == CB_MCG ? s * CBMCG_MUL : mad_lo(s, k.mul, CB3_ADD);
     }
     return (x & k.mask) ^ k.flip;
 }
