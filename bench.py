@@ -30,6 +30,7 @@ embedding gather of one batch-1 token as one HIP graph, replayed (attention excl
     python bench.py --workload config3   # M=2048 prefill GEMM (TFLOP/s, MFMA share) + reconstruct
     python bench.py --workload config4   # the 64-layer batch-1 linear stack alone (tok/s-equivalent)
     python bench.py --workload prefill   # 17..768-row prefill: fused vs reconstruct branch, grouped layers
+    python bench.py --workload ceiling   # what bounds batch 1: loads / decode / MFMA alone, instruction costs
 print their own JSON line instead of the headline line.
 """
 from __future__ import annotations
@@ -533,6 +534,87 @@ def cpu_baseline(runs: int = 5) -> dict:
                                   f"{threads} threads"}}
 
 
+CEILING_OPS = {1: "v_add_u32", 2: "v_bitop3_b32", 3: "v_lshrrev_b32", 4: "v_mul_lo_u32", 5: "v_bfe_u32",
+               6: "v_alignbit_b32", 7: "v_add_u32_sdwa", 8: "v_perm_b32", 9: "v_lshlrev_b32", 10: "v_mov_b32_dpp",
+               11: "v_mad_u64_u32", 12: "v_mfma_f32_4x4x4_16b_f16", 13: "v_mfma_f32_16x16x32_f16",
+               14: "4x4x4 MFMA waves beside v_mul_lo_u32 waves", 15: "16x16x32 MFMA waves beside v_mul_lo_u32 waves"}
+
+
+def ceiling_bench(reps: int) -> dict:
+    """What bounds the batch-1 GEMV (down_proj 17408 -> 5120): the measurement kernels of
+    libexl3ceiling.so walk the same units, workgroup ranges, wave runs and load ring as
+    gemv1_kernel but stop short of parts of its work (empty grid / loads only / loads +
+    three-instruction decode / loads + decode + the 16 MFMAs per unit with activations from a
+    constant LDS table), timed per call in HIP graphs over rotating weight copies exactly like
+    config 1, beside the product GEMV itself; then the issue cost of the decode's instructions
+    and of the MFMA forms (8 independent chains per wave, 8 waves per SIMD)."""
+    import ctypes
+    import torch
+    from orcasaq2 import _native
+    path = os.path.join(ROOT, "orcasaq2-kernel_amd", "orcasaq2", "libexl3ceiling.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built (python orcasaq2-kernel_amd/build_lib.py)")
+    M = ctypes.CDLL(path)
+    M.exl3m_stream.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                               ctypes.c_void_p, ctypes.c_void_p]
+    M.exl3m_ops.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    M.exl3m_sink_bytes.restype = ctypes.c_long
+    M.exl3m_stream_workgroups.argtypes = [ctypes.c_int, ctypes.c_int]
+    M.exl3m_sink_bytes.argtypes = [ctypes.c_int, ctypes.c_int]
+    dev = torch.device("cuda", 0)
+    ic, oc, calls = 17408, 5120, 30
+    sink = torch.empty(M.exl3m_sink_bytes(ic, oc), dtype=torch.uint8, device=dev)
+    g = torch.Generator(device=dev).manual_seed(7)
+    out, names = {}, ["empty grid", "loads only", "loads + decode", "loads + decode + MFMA (constant activations)",
+                      "same with 16x16x32 MFMAs"]
+    for K in (2, 3, 4, 5):
+        nbytes = ic * oc * K // 8
+        copies = [_rand_linear(ic, oc, K, g, dev) for _ in range(max(2, math.ceil(ROTATE_BYTES / nbytes)))]
+        x = torch.randn(1, ic, generator=g, device=dev).half()
+        y = torch.empty(1, oc, dtype=torch.half, device=dev)
+        row = {"bytes": nbytes}
+        for mode in range(5):
+            def run(mode=mode):
+                st = torch.cuda.current_stream(dev).cuda_stream
+                for i in range(calls):
+                    rc = M.exl3m_stream(mode, copies[i % len(copies)]["trellis"].data_ptr(), ic, oc, K,
+                                        sink.data_ptr(), st)
+                    if rc != 0:
+                        raise RuntimeError(f"exl3m_stream mode {mode} K={K}: {rc}")
+            gr, side = _graph(dev, run, settle=False)
+            us = _time_graph(gr, side, reps) / calls * 1e6
+            row[names[mode]] = {"us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1)}
+
+        def prod():
+            for i in range(calls):
+                d = copies[i % len(copies)]
+                _native.gemv(x, d["trellis"], d["suh"], d["svh"], K, 0, out=y)
+        gr, side = _graph(dev, prod)
+        us = _time_graph(gr, side, reps) / calls * 1e6
+        row["product gemv1_kernel"] = {"us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1)}
+        out[f"K={K}"] = row
+        del copies
+        torch.cuda.empty_cache()
+    iters, ops = 500, {}
+    waves_per_simd = 8
+    for op, name in CEILING_OPS.items():
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        st = torch.cuda.current_stream(dev).cuda_stream
+        M.exl3m_ops(op, 10, sink.data_ptr(), st)
+        best = 1e9
+        for _ in range(3):
+            e0.record()
+            if M.exl3m_ops(op, iters, sink.data_ptr(), st) != 0:
+                raise RuntimeError(f"exl3m_ops {op}")
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e-3)
+        ns = best * 1e9 / (waves_per_simd * iters * 32)
+        ops[name] = {"ns_per_wave_instr_per_simd": round(ns, 3), "cycles_at_2.1GHz": round(ns * 2.1, 2)}
+    return {"shape": "down_proj 17408->5120, batch 1, one shard per call, 30 calls per graph over rotating copies",
+            "per_call": out, "instruction_issue": ops}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -541,7 +623,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only-K", type=int, default=0, help="time a single K (profiling runs)")
     ap.add_argument("--copy-calib", action="store_true", help="run the counter-calibration copy and exit")
-    ap.add_argument("--workload", default="config1", choices=("config1", "config2", "config3", "config4", "prefill"),
+    ap.add_argument("--workload", default="config1",
+                    choices=("config1", "config2", "config3", "config4", "prefill", "ceiling"),
                     help="config1 = the headline line (+ the config-4 stack); config2/config3/config4 "
                          "print their own measurement line")
     ap.add_argument("--no-stack", action="store_true", help="skip the config-4 stack measurement")
@@ -554,9 +637,10 @@ def main():
     if args.copy_calib:
         copy_calib(args)
         return
-    if args.workload in ("config2", "config3", "config4", "prefill"):
+    if args.workload in ("config2", "config3", "config4", "prefill", "ceiling"):
         import torch
         res = (config2_bench(args.steps * 5) if args.workload == "config2" else
+               ceiling_bench(args.steps) if args.workload == "ceiling" else
                config3_bench(args.steps) if args.workload == "config3" else
                prefill_bench(args.steps) if args.workload == "prefill" else stack_bench(args.steps))
         print(json.dumps({"workload": args.workload, "results": res,

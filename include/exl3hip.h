@@ -19,11 +19,10 @@
  *     as EXL3_ERR_UNSUPPORTED.
  *   - Workspaces are caller-owned device buffers (256-byte aligned) of at least the
  *     *_workspace_bytes() size; a call uses its workspace until its last kernel has run,
- *     so calls that may overlap in time must not share one.  The GEMM workspace has no
- *     required contents.  A GEMV workspace starts with a 16 KiB counter area that must be
- *     zero-filled before its first use; every GEMV call that completes leaves it zero
- *     again, so one zeroed buffer serves any sequence of calls issued in order (one
- *     stream) -- also HIP-graph replays of captured calls.
+ *     so calls that may overlap in time must not share one.  Workspaces have no required
+ *     contents (a GEMV workspace starts with a reserved 16 KiB area that no call reads),
+ *     so one buffer serves any sequence of calls issued in order on one stream -- also
+ *     HIP-graph replays of captured calls.
  */
 #ifndef EXL3HIP_H
 #define EXL3HIP_H
@@ -92,8 +91,9 @@ int exl3_had_r_128(const void* in, void* out, const void* pre, const void* post,
  *   C (rows, oc) = fp16( H( fp16(H(A * suh)) . W_q ) * svh ),  A (rows, ic) fp16.
  * Replaces ext.exl3_gemm(A, trellis, C, suh, A_had, svh, -1, mcg, mul1, 0)
  * [orcasaq2/ops.py:46-49] for rows <= 16 (the A_had scratch is internal to the kernel).
- * The workspace (see the conventions above) must start zero-filled.  rows == 1 is one
- * kernel launch per (K, codebook) group; other row counts are two.
+ * rows 1..4 take one decode launch per codebook (followed, when a column group's inputs
+ * were split over several workgroups, by one small kernel that adds the split partial
+ * sums); 5..16 rows take a set-up kernel and one launch per codebook.
  */
 size_t exl3_gemv_workspace_bytes(int rows, int ic, int oc);
 int exl3_gemv(const void* A, const void* trellis, void* C, const void* suh, const void* svh,

@@ -18,6 +18,8 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "orcasaq2", "libexl3hip.so")
+MEASURE = os.path.join(CSRC, "measure")
+CEILING = os.path.join(HERE, "orcasaq2", "libexl3ceiling.so")
 ARCH = os.environ.get("EXL3_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -67,7 +69,25 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, OUT)
+    build_ceiling(verbose)
     return OUT
+
+
+def build_ceiling(verbose: bool = False) -> str:
+    """The measurement library of bench.py --workload ceiling (csrc/measure/*.hip): kernels
+    that walk a shard the way the batch-1 GEMV does but stop short of parts of its work, and
+    instruction-rate chains.  Not part of libexl3hip or its C ABI."""
+    cc = hipcc()
+    srcs = sorted(os.path.join(MEASURE, f) for f in os.listdir(MEASURE) if f.endswith(".hip"))
+    tmp = CEILING + ".tmp"
+    cmd = [cc] + HIPCC_FLAGS + ["-shared", "-o", tmp] + srcs
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for the measurement library:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, CEILING)
+    return CEILING
 
 
 if __name__ == "__main__":

@@ -291,24 +291,26 @@ __device__ __forceinline__ Dot2Consts dot2_consts()
     return k;
 }
 
+// Codebook word x = a*s + b (mod 2^32) of chunk position Q, before the mask.
+template <int K, int CB, int Q>
+__device__ __forceinline__ uint32_t dot2_raw(const uint32_t (&w)[K + 1], const Dot2Consts& k)
+{
+    using P = StatePlan<K, Q>;
+    if constexpr (P::kind <= 1) {
+        const uint32_t src = w[P::wi];
+        if constexpr (CB == CB_MCG) return (P::kind == 1 ? (src >> 16) : (src & 0xffffu)) * CBMCG_MUL;
+        else return (P::kind == 1 ? sdwa_add_hi(src, k.off) : sdwa_add_lo(src, k.off)) * CB3_MUL;
+    } else {
+        const uint32_t s = state_field<K, Q>(w);
+        return CB == CB_MCG ? s * CBMCG_MUL : mad_lo(s, k.mul, CB3_ADD);
+    }
+}
+
 // Masked codebook word of chunk position Q.
 template <int K, int CB, int Q>
 __device__ __forceinline__ uint32_t dot2_word(const uint32_t (&w)[K + 1], const Dot2Consts& k)
 {
-    using P = StatePlan<K, Q>;
-    uint32_t x;
-    if constexpr (P::kind <= 1) {
-        const uint32_t src = w[P::wi];
-        if constexpr (CB == CB_MCG) {
-            x = (P::kind == 1 ? (src >> 16) : (src & 0xffffu)) * CBMCG_MUL;
-        } else {
-            x = (P::kind == 1 ? sdwa_add_hi(src, k.off) : sdwa_add_lo(src, k.off)) * CB3_MUL;
-        }
-    } else {
-        const uint32_t s = state_field<K, Q>(w);
-        x = CB == CB_MCG ? s * CBMCG_MUL : mad_lo(s, k.mul, CB3_ADD);
-    }
-    return (x & k.mask) ^ k.flip;
+    return (dot2_raw<K, CB, Q>(w, k) & k.mask) ^ k.flip;
 }
 
 __device__ __forceinline__ float dot2_f16(uint32_t a, uint32_t b, float c)

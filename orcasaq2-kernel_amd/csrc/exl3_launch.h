@@ -29,15 +29,15 @@ struct GemvShard {
     long ldc;
 };
 
-// Start of every GEMV workspace: one u32 counter per column group of a batch-1 launch,
-// zero before the first call and left zero by every call (the batch-1 kernel resets the
-// counters it uses).  Partial-sum buffers of all GEMV paths start after it.
+// A reserved 16 KiB area at the head of every GEMV workspace (no kernel reads or writes it;
+// it keeps the published workspace layout and sizes).  The partial-sum buffers of all GEMV
+// paths start after it.
 constexpr size_t GEMV_COUNTER_BYTES = 16384;
 size_t gemv_workspace_bytes(int rows, int ic, int oc);
 size_t gemv1_slot_bytes(int ic, int oc, int rows);
 bool gemv1_rows_fit(const GemvShard* shards, int nshards);
-int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, uint32_t* counters,
-                   int max_counters, char* slots, size_t slot_bytes, hipStream_t stream);
+int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
+                   size_t slot_bytes, hipStream_t stream);
 int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows,
                   void* workspace, size_t ws_bytes, hipStream_t stream);
 size_t gemm_workspace_bytes(int rows, int ic, int oc);

@@ -71,7 +71,7 @@ static inline int gemv_splits(int ic, int oc)
 
 static inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Per-shard share of a GEMV workspace (the counter area is added once per call).
+// Per-shard share of a GEMV workspace (the reserved head area is added once per call).
 size_t gemv_workspace_bytes(int rows, int ic, int oc)
 {
     if (rows == 1) return align256(gemv1_slot_bytes(ic, oc, 1));
@@ -305,9 +305,8 @@ int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int r
 
     char* ws = static_cast<char*>(workspace);
     if (rows == 1 || (rows <= GV_SPLIT_MAX_ROWS && gemv1_rows_fit(shards, nshards)))
-        return gemv1_dispatch(A, shards, nshards, rows, reinterpret_cast<uint32_t*>(ws),
-                              (int)(GEMV_COUNTER_BYTES / sizeof(uint32_t)), ws + GEMV_COUNTER_BYTES,
-                              offs[nshards] - GEMV_COUNTER_BYTES, stream);
+        return gemv1_dispatch(A, shards, nshards, rows, ws + GEMV_COUNTER_BYTES, offs[nshards] - GEMV_COUNTER_BYTES,
+                              stream);
     if (rows > GV_SPLIT_MAX_ROWS)
         return gemv_sk_dispatch(A, shards, nshards, rows, ws + GEMV_COUNTER_BYTES, offs[nshards] - GEMV_COUNTER_BYTES,
                                 stream);

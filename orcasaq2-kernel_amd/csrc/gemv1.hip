@@ -19,21 +19,22 @@
 //      for every row r, into an LDS table of duplicated fp16 pairs;
 //   2. main loop over the run: a unit's data streams through the D-deep register ring.
 //      The tail-biting word before a lane's chunk is the previous lane's last word (DPP
-//      rotate within the tile's 8 lanes).  Each position is decoded with an SDWA add (or a
-//      16-bit field for MCG), a v_mul_lo_u32 and a v_bitop3; the masked words go into the
-//      B operand of v_mfma_f32_4x4x4_16b_f16 (each word's two fp16 halves as two k-slots
-//      against one activation twice, so lo * x + hi * x is summed in fp32) and the unit's
-//      activations into A: block row i (lane 4b + i) carries activation row i, so one MFMA
-//      serves up to four rows and column j (lane 4b + j) collects lane 4b + j's products;
+//      rotate within the tile's 8 lanes).  Each position is decoded with three VALU ops
+//      (dot2_word); the masked words go into the B operand of v_mfma_f32_16x16x32_f16
+//      (each word's two fp16 halves as two k-slots against one activation twice, so
+//      lo * x + hi * x is summed in fp32) and the unit's activations into A (g1_mfma16),
+//      one MFMA serving up to four activation rows.  A wave's priority steps down as its
+//      run progresses (s_setprio 3 -> 0): the sequencer otherwise issues the oldest waves
+//      first, the youngest workgroup on each CU starts its loop last, and the launch ends
+//      with that workgroup running alone;
 //   3. per segment, the waves' partial sums are added in a fixed order through LDS.  If the
-//      segment lies inside this workgroup's range it is finished here; otherwise the
-//      partial goes to this workgroup's slot with agent-coherent stores, and the last of the
-//      segment's workgroups to arrive (a relaxed agent-scope counter in the workspace) has
-//      its eight waves add all slots (a fixed partition and order: deterministic) and
-//      finishes: output Hadamard, * svh, fp16 store, counter back to 0.  No cache-wide
-//      release/acquire is used: the slots are written with agent-scope stores and read
-//      with agent-scope loads, and each writer waits for its stores to complete before it
-//      increments the counter.
+//      segment lies inside this workgroup's range it is finished here (output Hadamard,
+//      * svh, fp16 store); otherwise the partial goes to this workgroup's slot in the
+//      workspace, and gemv1_finish_kernel, enqueued right after the launch, adds each split
+//      segment's slots in workgroup order (deterministic) and finishes it.  The kernel
+//      boundary orders the slot stores before the reads: no counters, fences or waits
+//      inside the launch (measured on MI355X against a last-arriving-workgroup finish with
+//      agent-scope stores and a counter: 4-9% faster on every 27B projection shape).
 #include "exl3_common.h"
 #include "exl3_launch.h"
 
@@ -79,8 +80,7 @@ __device__ __forceinline__ int g1_div(int x, G1Div d)
 struct G1Group {
     const uint16_t* x;         // (nrows, ic) fp16
     int nrows;                 // activation rows, 1 .. R of the kernel
-    uint32_t* counters;        // one per segment; zero between calls
-    float* slots;              // (G + segments) x 128 fp32
+    float* slots;              // (G + segments) x R x 128 fp32 partials of split segments
     int U, G, ntr, nshards, nsegs;
     int q, r;                  // U = q G + r: workgroup g owns q + (g < r) units
     G1Div dntr, dq, dq1;       // division by ntr, q, q + 1
@@ -93,11 +93,12 @@ struct G1Args {
 };
 
 // A launch of several groups of one codebook, one K each: group i owns workgroups
-// gbeg[i] .. gbeg[i + 1] - 1 and shards sh0[i] .. sh0[i] + grp[i].nshards - 1.
+// gbeg[i] .. gbeg[i + 1] - 1 and shards sh0[i] .. sh0[i] + grp[i].nshards - 1; in the finish
+// kernel it owns blocks fbeg[i] .. fbeg[i] + grp[i].nsegs - 1 (one per segment).
 struct G1Multi {
     G1Group grp[G1_MAXSH];
     G1Shard sh[G1_MAXSH];
-    int gbeg[G1_MAXSH], sh0[G1_MAXSH], K[G1_MAXSH];
+    int gbeg[G1_MAXSH], sh0[G1_MAXSH], K[G1_MAXSH], fbeg[G1_MAXSH];
     int ngrp;
 };
 
@@ -172,32 +173,41 @@ __device__ __forceinline__ void g1_load(uint32_t (&w)[K + 1], const uint32_t* __
     }
 }
 
-// One lane's chunk (32 positions) multiplied into its two output columns with
-// v_mfma_f32_4x4x4_16b_f16: the activations go in A (the same for every lane, so each
-// 4-row block of A repeats them) and the lane's masked codebook words in B, each word's two
-// fp16 halves as two k-slots against one activation twice -- so the weight's fp16 half-sum
-// is never rounded, and block b's column n (lane 4b + n) collects only that lane's products.
-// MFMA J takes positions q0 = 8m + 2p + 4h and q0 + 1 (m = J / 4, p = J / 2 % 2, h = J % 2):
-// rows 2m + 8p and 2m + 8p + 1 of the tile row (act16 holds the 16 rows as duplicated fp16
-// pairs), output column half h (acc[h]).
-template <int K, int CB, int J>
-__device__ __forceinline__ void g1_mfma_pair(const uint32_t (&w)[K + 1], const uint32_t (&act16)[16], f32x4 (&acc)[2],
-                                             const Dot2Consts& kc)
+// One lane's chunk (32 positions) multiplied into its two output columns with eight
+// v_mfma_f32_16x16x32_f16.  The unit's 64 lanes are four groups j = l / 16 of two tiles
+// (tiles 2j, 2j + 1, one tile row); lane l supplies B column n = l % 16 of k-block j: the
+// masked codebook words of four positions, each word's two fp16 halves as two k-slots against
+// one activation twice -- so the weight's fp16 half-sum is never rounded.  MFMA (m, h) takes
+// positions 8m + 4h + t (t = 0..3): rows 2m + {0, 1, 8, 9} of the tile row, column c + 8h of
+// the chunk.  A row i = 4r + j holds activation row r of those four rows (duplicated) in
+// k-block j and zeros in the other k-blocks, so C row 4r + j sums group j alone: C[4r + j][n]
+// (lane 16r + n, element j) is activation row r's partial for output 32j + 16(n / 8) + n % 8
+// + 8h of the unit's 128.  The MFMA's long latency lets other waves' decode VALU work issue
+// beside it (on MI355X it hides most of its 15 cycles; a v_mfma_f32_4x4x4_16b_f16 form with
+// twice the instructions hid under half of its 8).
+template <int K, int CB, int M, int H>
+__device__ __forceinline__ void g1_mfma16(const uint32_t (&w)[K + 1], const f16x8& a, f32x4 (&acc)[2],
+                                          const Dot2Consts& kc)
 {
-    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-    typedef uint32_t u2 __attribute__((ext_vector_type(2)));
-    constexpr int m = J / 4, p = (J / 2) % 2, h = J % 2;
-    constexpr int q0 = 8 * m + 2 * p + 4 * h;
-    const u2 bv = {dot2_word<K, CB, q0>(w, kc), dot2_word<K, CB, q0 + 1>(w, kc)};
-    const u2 av = {act16[2 * m + 8 * p], act16[2 * m + 8 * p + 1]};
-    acc[h] = __builtin_amdgcn_mfma_f32_4x4x4f16(__builtin_bit_cast(h4, av), __builtin_bit_cast(h4, bv), acc[h], 0, 0, 0);
+    typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+    constexpr int q = 8 * M + 4 * H;
+    const u4 b = {dot2_word<K, CB, q>(w, kc), dot2_word<K, CB, q + 1>(w, kc), dot2_word<K, CB, q + 2>(w, kc),
+                  dot2_word<K, CB, q + 3>(w, kc)};
+    acc[H] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(f16x8, b), acc[H], 0, 0, 0);
 }
 
-template <int K, int CB, int... Js>
-__device__ __forceinline__ void g1_mfma_chunk(const uint32_t (&w)[K + 1], const uint32_t (&act16)[16], f32x4 (&acc)[2],
-                                              const Dot2Consts& kc, std::integer_sequence<int, Js...>)
+template <int K, int CB>
+__device__ __forceinline__ void g1_mfma_chunk(const uint32_t (&w)[K + 1], const f16x8 (&a)[4], f32x4 (&acc)[2],
+                                              const Dot2Consts& kc)
 {
-    (g1_mfma_pair<K, CB, Js>(w, act16, acc, kc), ...);
+    g1_mfma16<K, CB, 0, 0>(w, a[0], acc, kc);
+    g1_mfma16<K, CB, 0, 1>(w, a[0], acc, kc);
+    g1_mfma16<K, CB, 1, 0>(w, a[1], acc, kc);
+    g1_mfma16<K, CB, 1, 1>(w, a[1], acc, kc);
+    g1_mfma16<K, CB, 2, 0>(w, a[2], acc, kc);
+    g1_mfma16<K, CB, 2, 1>(w, a[2], acc, kc);
+    g1_mfma16<K, CB, 3, 0>(w, a[3], acc, kc);
+    g1_mfma16<K, CB, 3, 1>(w, a[3], acc, kc);
 }
 
 __device__ __forceinline__ uint32_t g1_dup(float v)
@@ -220,6 +230,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     const int ub = g1_first_unit(a, g), L = a.q + (g < a.r ? 1 : 0);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
+    __builtin_amdgcn_s_setprio(3);
 
     // ---- this wave's units: the contiguous run ub + lo .. ub + lo + n - 1 of the range
     const int lo = (wave * L) >> 3;
@@ -310,10 +321,11 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     }();
 
     // LDS: red[nseg][G1_NW][R][128] fp32 partial rows | act[nocc][8][R][16] duplicated fp16
-    // activations | last[nseg]
+    // activations | zero[16] (the A operand of the lanes whose k-block is not theirs)
     float* red = reinterpret_cast<float*>(lds);
     uint32_t* act = reinterpret_cast<uint32_t*>(red + nseg * G1_NW * R * 128);
-    int* last = reinterpret_cast<int*>(act + nocc * R * 128);
+    uint32_t* zero = act + nocc * R * 128;
+    if (threadIdx.x < 16) zero[threadIdx.x] = 0u;
     for (int k = 0; k < nseg; k++)
 #pragma unroll
         for (int r = 0; r < R; r++)
@@ -324,9 +336,10 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     // Activations, once per workgroup while the first trellis loads are in flight: the waves
     // share out the occurrences; each transforms its block of every activation row r,
     // fp16(H128(x_r * suh)) (lane l: outputs 2l, 2l + 1 = rows 2(l % 8), 2(l % 8) + 1 of the
-    // block's tile row l / 8) and stores each output as a duplicated fp16 pair:
-    // act[occurrence][tile row][r][row].  Rows r >= nrows repeat the last row (their
-    // results are not stored).
+    // block's tile row l / 8) and stores each output as a duplicated fp16 pair in the order
+    // the MFMAs read them: act[occurrence][tile row][r][m][t] holds row 2m + {0, 1, 8, 9}[t]
+    // (so lane l's two rows go to m = l % 4, t = 2 ((l % 8) / 4) and t + 1).  Rows
+    // r >= nrows repeat the last row (their results are not stored).
     for (int i = wave; i < nocc; i += G1_NW) {
         int k = 0, blk = (tr0 >> 3) + i;
         if (i >= nb0) {
@@ -341,7 +354,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
             const uint32_t xw = reinterpret_cast<const uint32_t*>(a.x + min(r, a.nrows - 1) * ic + blk * 128)[lane];
             float v0 = g1_lo(xw) * g1_lo(sw), v1 = g1_hi(xw) * g1_hi(sw);
             wave_fwht128(v0, v1);
-            *reinterpret_cast<uint2*>(act + ((i * 8 + (lane >> 3)) * R + r) * 16 + 2 * (lane & 7)) =
+            *reinterpret_cast<uint2*>(act + ((i * 8 + (lane >> 3)) * R + r) * 16 + 4 * (lane & 3) + 2 * ((lane >> 2) & 1)) =
                 uint2{g1_dup(v0), g1_dup(v1)};
         }
     }
@@ -353,18 +366,28 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     // so the wait before a unit covers only that unit's own loads.  The occurrence index
     // steps whenever a unit starts a block (its tile row a multiple of 8, which includes
     // every segment start).
-    const int o0 = (lane >> 3) * 16 + (lane & 7);
-    // yacc[h][r]: activation row r's sum for column o0 + 8 h (rows r >= R are copies)
+    // yacc[h][e] of lane 16r + n: activation row r's sum for output 32e + 16(n / 8) + n % 8 + 8h
+    // (lanes 16r + n with r >= R hold copies of row R - 1).
     f32x4 yacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    // the activation row this lane feeds into the MFMAs' A operand (A row = lane % 4)
-    const int arow = R == 1 ? 0 : min(lane & 3, R - 1);
+    const int yrow = lane >> 4, ycol = 16 * ((lane >> 3) & 1) + (lane & 7);
+    // This lane's A operand: row i = lane % 16 in k-block lane / 16, which carries activation
+    // row i / 4 when i % 4 is that k-block and zeros otherwise.  Its LDS byte address for a
+    // unit whose table entry starts at byte e: e * asel + aoff.
+    const uint32_t asel = ((lane & 15) & 3) == (lane >> 4) ? 1u : 0u;
+    const uint32_t aoff = asel ? (uint32_t)((reinterpret_cast<char*>(act) - reinterpret_cast<char*>(lds)) +
+                                            min((lane & 15) >> 2, R - 1) * 64)
+                               : (uint32_t)(reinterpret_cast<char*>(zero) - reinterpret_cast<char*>(lds));
     int cur = cu.S - S_first;
     int occ = occ_of(cur, cu.tr);
+    const int pq1 = (n + 3) >> 2, pq2 = (n + 1) >> 1, pq3 = (3 * n + 3) >> 2;
     auto flush = [&](int k) {
+        if (yrow < R) {
+            float* rr = red + ((cur * G1_NW + wave) * R + yrow) * 128 + ycol;
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            red[((cur * G1_NW + wave) * R + r) * 128 + o0] = yacc[0][r];
-            red[((cur * G1_NW + wave) * R + r) * 128 + o0 + 8] = yacc[1][r];
+            for (int e = 0; e < 4; e++) {
+                rr[32 * e] = yacc[0][e];
+                rr[32 * e + 8] = yacc[1][e];
+            }
         }
         yacc[0] = yacc[1] = f32x4{0.f, 0.f, 0.f, 0.f};
         cur = k;
@@ -374,23 +397,25 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         for (int d = 0; d < D; d++) {
             if (d == 0 || j + d < n) {
                 if (cu.S - S_first != cur) flush(cu.S - S_first);
-                const uint4* ap = reinterpret_cast<const uint4*>(act + ((occ * 8 + (cu.tr & 7)) * R + arow) * 16);
-                uint32_t act16[16];
-#pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    const uint4 t = ap[v];
-                    act16[4 * v] = t.x; act16[4 * v + 1] = t.y; act16[4 * v + 2] = t.z; act16[4 * v + 3] = t.w;
-                }
+                const uint32_t e = (uint32_t)((occ * 8 + (cu.tr & 7)) * R) * 64u;
+                const f16x8* ap = reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(lds) + (__umul24(e, asel) + aoff));
+                const f16x8 av[4] = {ap[0], ap[1], ap[2], ap[3]};
                 chunk_prev_dpp<K>(ring[d].w, first_lane);
-                g1_mfma_chunk<K, CB>(ring[d].w, act16, yacc, kc, std::make_integer_sequence<int, 16>{});
+                g1_mfma_chunk<K, CB>(ring[d].w, av, yacc, kc);
                 if (j + d + 1 < n) {
                     advance(cu);
                     occ += (cu.tr & 7) == 0;
                 }
+                // priority 3, 2, 1, 0 over the run's four quarters
+                const int done = j + d + 1;
+                if (done == pq1) __builtin_amdgcn_s_setprio(2);
+                if (done == pq2) __builtin_amdgcn_s_setprio(1);
+                if (done == pq3) __builtin_amdgcn_s_setprio(0);
             }
             load(ring[d], next_pf());
         }
     }
+    __builtin_amdgcn_s_setprio(3);
     if (n > 0) flush(cur);
     __syncthreads();
 
@@ -415,7 +440,6 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         g_hi = g1_wg_of(a, segU0 + ntr - 1);
     };
     const int nr = R == 1 ? 1 : a.nrows;
-    bool any_last = false;
     for (int k = wave; k < nseg; k += G1_NW) {
         float v0[R], v1[R];
 #pragma unroll
@@ -430,77 +454,16 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         }
         int g_lo, g_hi;
         contributors(k, g_lo, g_hi);
-        int is_last = 0;
         if (g_hi > g_lo) {
-            // slot (S + g) holds R rows of 128 partials
+            // split segment: slot (S + g) holds this workgroup's R rows of 128 partials, which
+            // gemv1_finish_kernel adds after the launch
             uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + (long)(S_first + k + g) * R * 128) + lane;
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint64_t pv = (uint64_t)__builtin_bit_cast(uint32_t, v0[r]) |
-                                    ((uint64_t)__builtin_bit_cast(uint32_t, v1[r]) << 32);
-                __hip_atomic_store(my + r * 64, pv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __builtin_amdgcn_s_waitcnt(0);   // this wave's slot stores are complete
-            uint32_t old = 0;
-            if (lane == 0)
-                old = __hip_atomic_fetch_add(a.counters + S_first + k, 1u, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT);
-            old = __shfl(old, 0, 64);
-            // last to arrive: every other contributor's slot stores completed before its
-            // counter increment, which precedes ours
-            is_last = old == (uint32_t)(g_hi - g_lo);
-            if (is_last && lane == 0)
-                __hip_atomic_store(a.counters + S_first + k, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int r = 0; r < R; r++)
+                my[r * 64] = (uint64_t)__builtin_bit_cast(uint32_t, v0[r]) |
+                             ((uint64_t)__builtin_bit_cast(uint32_t, v1[r]) << 32);
         } else {
             for (int r = 0; r < nr; r++) finish(k, r, v0[r], v1[r]);
-        }
-        if (lane == 0) last[k] = is_last;
-        any_last |= is_last != 0;
-    }
-    // Segments this workgroup completes for everyone: the eight waves add the slots (wave w
-    // takes slots g_lo + w, g_lo + w + 8, ... in order), then wave k adds the eight sums.
-    if (__syncthreads_or(any_last)) {
-        for (int k = 0; k < nseg; k++) {
-            if (!last[k]) continue;
-            int g_lo, g_hi;
-            contributors(k, g_lo, g_hi);
-            const int nsl = g_hi - g_lo + 1;
-            const uint64_t* sl = reinterpret_cast<const uint64_t*>(a.slots + (long)(S_first + k + g_lo) * R * 128) + lane;
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                float v0 = 0.f, v1 = 0.f;
-                for (int t0 = wave; t0 < nsl; t0 += 8 * G1_NW) {
-                    uint64_t xv[8];
-#pragma unroll
-                    for (int t = 0; t < 8; t++) {
-                        const int gg = min(t0 + t * G1_NW, nsl - 1);
-                        xv[t] = __hip_atomic_load(sl + ((long)gg * R + r) * 64, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-                    }
-#pragma unroll
-                    for (int t = 0; t < 8; t++) {
-                        if (t0 + t * G1_NW < nsl) {
-                            v0 += __builtin_bit_cast(float, (uint32_t)xv[t]);
-                            v1 += __builtin_bit_cast(float, (uint32_t)(xv[t] >> 32));
-                        }
-                    }
-                }
-                *reinterpret_cast<float2*>(red + ((k * G1_NW + wave) * R + r) * 128 + 2 * lane) = float2{v0, v1};
-            }
-        }
-        __syncthreads();
-        for (int k = wave; k < nseg; k += G1_NW) {
-            if (!last[k]) continue;
-            for (int r = 0; r < nr; r++) {
-                float v0 = 0.f, v1 = 0.f;
-#pragma unroll
-                for (int ww = 0; ww < G1_NW; ww++) {
-                    const float2 p = *reinterpret_cast<const float2*>(red + ((k * G1_NW + ww) * R + r) * 128 + 2 * lane);
-                    v0 += p.x;
-                    v1 += p.y;
-                }
-                finish(k, r, v0, v1);
-            }
         }
     }
 }
@@ -542,6 +505,72 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     case 7: g1_body<7, CB, false, R>(a, sht, g, lds); break;
     case 8: g1_body<8, CB, false, R>(a, sht, g, lds); break;
     }
+}
+
+// ---------------------------------------------------------------- finish kernel
+
+// Segment S of group a (shards sht), if a launch split it over several workgroups: its slots
+// (written by the launch just before, on the same stream) added in workgroup order -- the
+// same order on every call: deterministic -- then the output Hadamard, * svh and the fp16
+// store, by one wave.  A segment inside one workgroup's range was finished by that
+// workgroup.  Up to 32 slots are loaded per batch, all before the first add, so a segment
+// split over <= 32 workgroups costs one round trip to memory.
+template <int R, bool ONE>
+__device__ __forceinline__ void g1_finish_body(const G1Group& a, const G1Shard* sht, int S)
+{
+    auto sh = [&](int s) -> const G1Shard& { return sht[ONE ? 0 : s]; };
+    if (S >= a.nsegs) return;
+    const int s = g1_shard_of_seg<ONE>(a, sht, S);
+    const int cg = S - sh(s).sbeg;
+    const int segU0 = sh(s).ubeg + cg * a.ntr;
+    const int g_lo = g1_wg_of(a, segU0), g_hi = g1_wg_of(a, segU0 + a.ntr - 1);
+    if (g_hi == g_lo) return;
+    const int lane = threadIdx.x;
+    const int nsl = g_hi - g_lo + 1;
+    const int nr = R == 1 ? 1 : a.nrows;
+    const uint32_t sv = reinterpret_cast<const uint32_t*>(sh(s).svh + cg * 128)[lane];
+    const uint64_t* sl = reinterpret_cast<const uint64_t*>(a.slots + (long)(S + g_lo) * R * 128) + lane;
+    constexpr int B = 32;
+    for (int r = 0; r < nr; r++) {
+        float v0 = 0.f, v1 = 0.f;
+        for (int t0 = 0; t0 < nsl; t0 += B) {
+            uint64_t xv[B];
+#pragma unroll
+            for (int t = 0; t < B; t++) xv[t] = sl[((long)min(t0 + t, nsl - 1) * R + r) * 64];
+#pragma unroll
+            for (int t = 0; t < B; t++)
+                if (t0 + t < nsl) {
+                    v0 += __builtin_bit_cast(float, (uint32_t)xv[t]);
+                    v1 += __builtin_bit_cast(float, (uint32_t)(xv[t] >> 32));
+                }
+        }
+        wave_fwht128(v0, v1);
+        v0 *= g1_lo(sv);
+        v1 *= g1_hi(sv);
+        reinterpret_cast<uint32_t*>(sh(s).C + r * sh(s).ldc + cg * 128)[lane] =
+            (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
+    }
+}
+
+// A single-group launch's split segments (block = segment): every argument field is read at
+// a constant offset, so its scalar loads issue together.
+template <int R, bool ONE>
+__global__ __launch_bounds__(64) void gemv1_finish_kernel(const G1Args a)
+{
+    g1_finish_body<R, ONE>(a.grp, a.sh, blockIdx.x);
+}
+
+// A multi-group launch's split segments: block b is segment b - fbeg[i] of group i.
+template <int R>
+__global__ __launch_bounds__(64) void gemv1_finish_multi_kernel(const G1Multi)
+{
+    const G1Multi& mm = *(const G1Multi*)__builtin_amdgcn_kernarg_segment_ptr();
+    int i = 0;
+#pragma unroll
+    for (int j = 1; j < G1_MAXSH; j++)
+        if (j < mm.ngrp && (int)blockIdx.x >= mm.fbeg[j]) i = j;
+    i = __builtin_amdgcn_readfirstlane(i);
+    g1_finish_body<R, false>(mm.grp[i], mm.sh + mm.sh0[i], blockIdx.x - mm.fbeg[i]);
 }
 
 // ---------------------------------------------------------------- host side
@@ -587,17 +616,17 @@ static G1Div g1_magic(uint32_t d)
     return G1Div{(uint32_t)(((1ull << (31 + l)) / d) + 1), l - 1};
 }
 
-// Dynamic LDS a launch needs: a partial row per wave and a flag for the most segments
-// (shard, column group) a workgroup range of ceil(U / G) units can touch, and a transformed
-// activation block for each 128-input block it can meet (at most ceil(L / 8) + nseg + 1:
-// a piece of a segment meets one block more than its length in blocks when it starts
-// inside a block, and only the first piece can).
+// Dynamic LDS a launch needs: a partial row per wave for the most segments (shard, column
+// group) a workgroup range of ceil(U / G) units can touch, a transformed activation block for
+// each 128-input block it can meet (at most ceil(L / 8) + nseg + 1: a piece of a segment
+// meets one block more than its length in blocks when it starts inside a block, and only the
+// first piece can), and the 64-byte zero operand.
 static size_t g1_lds_bytes(int U, int G, int ntr, int R)
 {
     const int L = (U + G - 1) / G;
     const int nseg = (L - 1 + ntr - 1) / ntr + 1;
     const int nocc = (L + 7) / 8 + nseg + 1;
-    return (size_t)nseg * (G1_NW * R * 128 * sizeof(float) + 4) + (size_t)nocc * R * 128 * sizeof(uint32_t);
+    return (size_t)nseg * G1_NW * R * 128 * sizeof(float) + (size_t)nocc * R * 128 * sizeof(uint32_t) + 64;
 }
 
 // Row-count template of a call: one activation row, or up to four (G1_ROWS).
@@ -649,15 +678,11 @@ static long g1_group(G1Group& grp, G1Shard* tab, const GemvShard* shards, const 
     return U;
 }
 
-// Workgroup split of a group of U units into G ranges, and its share of counters and slots.
-static int g1_place(G1Group& grp, long U, int G, int R, uint32_t* counters, int& cbase, int max_counters, char* slots,
-                    size_t& sbase, size_t slot_bytes)
+// Workgroup split of a group of U units into G ranges, and its share of the slots.
+static int g1_place(G1Group& grp, long U, int G, int R, char* slots, size_t& sbase, size_t slot_bytes)
 {
     if (U > (1L << 30))
         return set_error(EXL3_ERR_ARG, "exl3_gemv: %ld tile-row units in one launch (limit 2^30)", U);
-    if (cbase + grp.nsegs > max_counters)
-        return set_error(EXL3_ERR_ARG, "exl3_gemv: %d column groups exceed the %d segment counters",
-                         cbase + grp.nsegs, max_counters);
     const size_t need = (size_t)(G + grp.nsegs) * R * 128 * sizeof(float);
     if (sbase + need > slot_bytes)
         return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: slot area of %zu bytes, %zu needed", slot_bytes,
@@ -670,11 +695,52 @@ static int g1_place(G1Group& grp, long U, int G, int R, uint32_t* counters, int&
     grp.dntr = g1_magic((uint32_t)grp.ntr);
     grp.dq = g1_magic((uint32_t)grp.q);
     grp.dq1 = g1_magic((uint32_t)grp.q + 1);
-    grp.counters = counters + cbase;
     grp.slots = reinterpret_cast<float*>(slots + sbase);
-    cbase += grp.nsegs;
     sbase += need;
     return EXL3_OK;
+}
+
+// Whether some segment of the group lies in more than one workgroup range (then the
+// launch needs gemv1_finish_kernel): segment S is units S ntr .. S ntr + ntr - 1.
+static bool g1_any_split(const G1Group& grp)
+{
+    const long big = (long)grp.r * (grp.q + 1);
+    auto wg_of = [&](long u) { return u < big ? u / (grp.q + 1) : grp.r + (u - big) / grp.q; };
+    for (int S = 0; S < grp.nsegs; S++)
+        if (wg_of((long)S * grp.ntr) != wg_of((long)S * grp.ntr + grp.ntr - 1)) return true;
+    return false;
+}
+
+// The finish kernel of a single-group launch, if any of its segments is split.
+static int g1_finish(G1Args& args, int R, bool one, hipStream_t stream)
+{
+    if (!g1_any_split(args.grp)) return EXL3_OK;
+    const void* fn = R == 1 ? (one ? reinterpret_cast<const void*>(&gemv1_finish_kernel<1, true>)
+                                   : reinterpret_cast<const void*>(&gemv1_finish_kernel<1, false>))
+                            : (one ? reinterpret_cast<const void*>(&gemv1_finish_kernel<G1_ROWS, true>)
+                                   : reinterpret_cast<const void*>(&gemv1_finish_kernel<G1_ROWS, false>));
+    void* kargs[] = {&args};
+    hipLaunchKernel(fn, dim3(args.grp.nsegs), dim3(64), kargs, 0, stream);
+    return check_launch("exl3_gemv (1-4 rows, split segments)");
+}
+
+// The finish kernel of a multi-group launch (m.grp[0 .. m.ngrp - 1], m.sh, m.sh0 set), if any
+// of its segments is split.
+static int g1_finish(G1Multi& m, int R, hipStream_t stream)
+{
+    bool any = false;
+    int nb = 0;
+    for (int t = 0; t < m.ngrp; t++) {
+        m.fbeg[t] = nb;
+        nb += m.grp[t].nsegs;
+        any = any || g1_any_split(m.grp[t]);
+    }
+    if (!any) return EXL3_OK;
+    const void* fn = R == 1 ? reinterpret_cast<const void*>(&gemv1_finish_multi_kernel<1>)
+                            : reinterpret_cast<const void*>(&gemv1_finish_multi_kernel<G1_ROWS>);
+    void* kargs[] = {&m};
+    hipLaunchKernel(fn, dim3(nb), dim3(64), kargs, 0, stream);
+    return check_launch("exl3_gemv (1-4 rows, split segments)");
 }
 
 static int g1_launch(const void* fn, void* arg, int G, size_t lds, hipStream_t stream)
@@ -741,8 +807,8 @@ bool gemv1_rows_fit(const GemvShard* shards, int nshards)
 // workgroup counts scaled to the resident limit together.  Workgroups per CU: four, or
 // fewer where a launch's LDS per workgroup (larger with four rows) would not let four
 // stay resident.
-int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, uint32_t* counters,
-                   int max_counters, char* slots, size_t slot_bytes, hipStream_t stream)
+int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
+                   size_t slot_bytes, hipStream_t stream)
 {
     if (rows < 1 || rows > G1_ROWS) return set_error(EXL3_ERR_ARG, "exl3_gemv: rows=%d is not in 1..%d", rows, G1_ROWS);
     const int R = g1_R(rows);
@@ -766,7 +832,6 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int 
         gidx[j][gn[j]++] = i;
     }
 
-    int cbase = 0;
     size_t sbase = 0;
     bool done[MAXG] = {false};
     for (int j0 = 0; j0 < ng; j0++) {
@@ -796,17 +861,19 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int 
             G1Args args = {};
             args.grp = m.grp[0];
             for (int i = 0; i < gn[sel[0]]; i++) args.sh[i] = m.sh[i];
-            int rc = g1_place(args.grp, U[0], G[0], R, counters, cbase, max_counters, slots, sbase, slot_bytes);
+            int rc = g1_place(args.grp, U[0], G[0], R, slots, sbase, slot_bytes);
             if (rc != EXL3_OK) return rc;
             const bool one = gn[sel[0]] == 1;
             const void* fn = R == 1 ? g1_fn_kcb<1>(gK[sel[0]], cb, one) : g1_fn_kcb<G1_ROWS>(gK[sel[0]], cb, one);
             rc = g1_launch(fn, &args, G[0], lds, stream);
             if (rc != EXL3_OK) return rc;
+            rc = g1_finish(args, R, one, stream);
+            if (rc != EXL3_OK) return rc;
             continue;
         }
         int gb = 0;
         for (int t = 0; t < ns; t++) {
-            const int rc = g1_place(m.grp[t], U[t], G[t], R, counters, cbase, max_counters, slots, sbase, slot_bytes);
+            const int rc = g1_place(m.grp[t], U[t], G[t], R, slots, sbase, slot_bytes);
             if (rc != EXL3_OK) return rc;
             m.gbeg[t] = gb;
             gb += G[t];
@@ -816,7 +883,9 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int 
                                                : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST, 1>))
                                 : (cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG, G1_ROWS>)
                                                : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST, G1_ROWS>));
-        const int rc = g1_launch(fn, &m, gb, lds, stream);
+        int rc = g1_launch(fn, &m, gb, lds, stream);
+        if (rc != EXL3_OK) return rc;
+        rc = g1_finish(m, R, stream);
         if (rc != EXL3_OK) return rc;
     }
     return EXL3_OK;

@@ -7,9 +7,8 @@
 // Host code never passes the array's name to a kernel: that name is a host-side stand-in,
 // not a device address.  The first call on a device resolves the device address with
 // hipGetSymbolAddress (that device current) and keeps it; every later call uses the kept
-// pointer.  The first call also clears the counter area at the head of the array with a
-// fill kernel (never hipMemsetAsync: a memset node recorded into a graph has given wrong
-// results on replay).  Every call that completes leaves the counters zero again.
+// pointer.  The workspace has no required contents (include/exl3hip.h), so nothing is
+// cleared.
 //
 // All calls on one GPU share its array: calls that may overlap in time (different streams
 // without ordering between them, or graphs replayed concurrently) race on it.
@@ -26,15 +25,8 @@ constexpr int NA_MAX_DEVICES = 64;
 static void* g_scratch_ptr[NA_MAX_DEVICES];
 static std::mutex g_scratch_mu;
 
-__global__ void na_zero_kernel(uint32_t* p, int n)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) p[i] = 0u;
-}
-
-// Device address of this device's `scratch`, resolved and its counters cleared on the
-// device's first call (enqueued on `stream`, ahead of the call's own kernels).
-static int na_scratch(void** out, hipStream_t stream)
+// Device address of this device's `scratch`, resolved on the device's first call.
+static int na_scratch(void** out)
 {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -48,10 +40,6 @@ static int na_scratch(void** out, hipStream_t stream)
         if (e != hipSuccess || !p)
             return set_error(EXL3_ERR_HIP, "exl3_gemv_grouped_static: hipGetSymbolAddress(scratch): %s",
                              hipGetErrorString(e));
-        const int n = (int)(GEMV_COUNTER_BYTES / sizeof(uint32_t));
-        hipLaunchKernelGGL(na_zero_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, static_cast<uint32_t*>(p), n);
-        const int rc = check_launch("exl3_gemv_grouped_static (clear)");
-        if (rc != EXL3_OK) return rc;
         g_scratch_ptr[dev] = p;
     }
     *out = g_scratch_ptr[dev];
@@ -78,7 +66,7 @@ extern "C" int exl3_gemv_grouped_static(const void* A, const exl3_shard_t* shard
                          "maximum of %zu (EXL3_STATIC_SCRATCH_BYTES); use exl3_gemv_grouped with a workspace",
                          need, (size_t)EXL3_STATIC_SCRATCH_BYTES);
     void* ws = nullptr;
-    const int rc = na_scratch(&ws, static_cast<hipStream_t>(stream));
+    const int rc = na_scratch(&ws);
     if (rc != EXL3_OK) return rc;
     return exl3_gemv_grouped(A, shards, nshards, ws, (size_t)EXL3_STATIC_SCRATCH_BYTES, rows, ic, stream);
 }

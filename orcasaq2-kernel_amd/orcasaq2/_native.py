@@ -161,14 +161,12 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
-# GEMV workspaces.  A workspace's counter area must be zero when a call starts, and every
-# call that completes leaves it zero again, so one buffer serves every call issued in
-# order on one stream.
-#   _gemv_ws[(device, stream)]            made by an eager call: zero-filled at once.
+# GEMV workspaces.  A workspace has no required contents; one buffer serves every call
+# issued in order on one stream.
+#   _gemv_ws[(device, stream)]            made by an eager call.
 #   _gemv_ws_cap[(device, stream, id)]    made inside graph capture `id` because the
-#                                         stream had no large-enough eager workspace: its
-#                                         zero-fill is a node of that graph (run at every
-#                                         replay, before the calls that use it), so it is
+#                                         stream had no large-enough eager workspace (its
+#                                         memory comes from that graph's pool), so it is
 #                                         used by that capture only.
 # A workspace that a captured graph uses is never freed (_gemv_ws_kept): the graph's
 # replays keep writing to it after the eager side has moved on to a larger buffer.
@@ -201,7 +199,7 @@ def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
             if ws is None or ws.numel() < nbytes:
                 if ws is not None:
                     _gemv_ws_kept.append(ws)
-                ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+                ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
                 _gemv_ws_cap[ckey] = ws
                 _gemv_ws_kept.append(ws)
             return ws
@@ -210,7 +208,7 @@ def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
             _gemv_ws_kept.append(ws)
         return ws
     if ws is None or ws.numel() < nbytes:
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _gemv_ws[key] = ws
     return ws
 

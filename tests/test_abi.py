@@ -108,7 +108,7 @@ def test_workspace_sizes(native):
     arr = (native.Shard * 2)()
     arr[0].oc, arr[1].oc = 6144, 1024
     g = L.exl3_gemv_grouped_workspace_bytes(arr, 2, 4, 5120)
-    # the counter area (16 KiB) leads every GEMV workspace once; shards add their shares
+    # the reserved 16 KiB area leads every GEMV workspace once; shards add their shares
     counter = 16384
     assert g == (L.exl3_gemv_workspace_bytes(4, 5120, 6144) + L.exl3_gemv_workspace_bytes(4, 5120, 1024)
                  - counter)

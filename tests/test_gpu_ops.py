@@ -66,10 +66,10 @@ def _two_shard_step(rows, ic=1024):
 @pytest.mark.parametrize("rows", [1, 2, 9, 40])
 def test_hip_graph_capture_replays(native, oracle, rows):
     """The op and the grouped op captured into a HIP graph on a stream that ran them eagerly
-    first (so the capture uses that stream's eager, zero-filled GEMV workspace), replayed four
-    times with eager work between replays, against eager results: 1 row (persistent kernel,
-    its counters rearmed by every call), 2 rows (four-row template), 9 rows (16-row tiles, one
-    launch over both K), 40 rows (prefill: 48-row stream-K tiles, counters zeroed by the
+    first (so the capture uses that stream's eager GEMV workspace), replayed four times with
+    eager work between replays, against eager results: 1 row (persistent decode launch and
+    its split-segment finishing kernel), 2 rows (four-row template), 9 rows (16-row tiles,
+    one launch over both K), 40 rows (prefill: 48-row stream-K tiles, counters zeroed by the
     set-up kernels inside the graph)."""
     step = _two_shard_step(rows)
     x = syn.activations(rows, 1024, torch.Generator().manual_seed(1)).to(D)
@@ -129,8 +129,8 @@ def test_graphs_share_workspace_and_survive_its_growth(native):
 
 def test_capture_without_eager_warmup(native):
     """A capture on a stream that never ran the op eagerly: the workspace is made inside the
-    capture (its zero-fill a node of the graph) and is private to that graph; eager calls on
-    the same stream afterwards get their own, and both stay correct in any order."""
+    capture (from the graph's memory pool) and is private to that graph; eager calls on the
+    same stream afterwards get their own, and both stay correct in any order."""
     step = _two_shard_step(1)
     x = syn.activations(1, 1024, torch.Generator().manual_seed(21)).to(D)
     eager = step(x)
