@@ -14,10 +14,11 @@
 // *segments* (shard, column group); its eight waves take eight contiguous runs of it.
 //
 // Per wave:
-//   1. issue the loads of its first D units (D = 2..6 by K); while they are in flight the
-//      workgroup transforms the activation blocks its range meets, fp16(H128(x_r * suh))
-//      for every row r, into an LDS table of duplicated fp16 pairs;
-//   2. main loop over the run: a unit's data streams through the D-deep register ring.
+//   1. issue the loads of its first unit; while they are in flight the workgroup transforms
+//      the activation blocks its range meets, fp16(H128(x_r * suh)) for every row r, into an
+//      LDS table of duplicated fp16 pairs;
+//   2. main loop over the run: each unit's loads are issued in the previous unit's
+//      iteration (g1_depth: one unit in flight per wave, eight waves per SIMD).
 //      The tail-biting word before a lane's chunk is the previous lane's last word (DPP
 //      rotate within the tile's 8 lanes).  Each position is decoded with three VALU ops
 //      (dot2_word); the masked words go into the B operand of v_mfma_f32_16x16x32_f16
@@ -45,9 +46,12 @@ constexpr int G1_MAXSH = 8;              // shards per launch
 constexpr int G1_WG_PER_CU = 4;          // target resident workgroups per CU (8 waves / SIMD)
 constexpr int G1_GMAX = 2048;            // workgroups per launch (bounds the slot area)
 
-// Prefetch depth in units: about 24 VGPRs of loads in flight per lane whatever K is (a unit
-// is K trellis words and an activation pair per lane), 2..6 units.
-constexpr int g1_depth(int K) { return (24 / (K + 3)) < 2 ? 2 : (24 / (K + 3)) > 6 ? 6 : (24 / (K + 3)); }
+// Units a wave keeps in flight: one.  Eight waves per SIMD already keep enough loads in
+// flight, and every unit more per wave lengthens the memory queues that a launch's first
+// units and activation loads wait behind: measured on MI355X (down_proj, per call), depth 1
+// against 2 and against 24 / (K + 3) clamped to 2..6: K = 2 18.6 / 18.7 / 19.6 us, K = 3
+// 18.9 / 19.6 / 20.9, K = 4 19.4 / 19.8 / 20.7, K = 5 19.4 / 20.4 / 21.4.
+constexpr int g1_depth(int) { return 1; }
 
 struct G1Shard {
     const uint32_t* trellis;   // (ic/16, oc/16, 8K) u32
@@ -276,6 +280,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
 
     // A unit's loads: the lane's K words.  Prefetch cursor (D units ahead; it stops at the
     // wave's last unit, whose data is then loaded again and not used) and processing cursor.
+    // D = g1_depth(K) = 1 on MI355X; the ring stays general.
     struct Slot {
         uint32_t w[K + 1];
     };
