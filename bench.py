@@ -14,9 +14,9 @@ replays its steps), so host launch overhead is not part of the measurement; the
 warm-up steps are a graph replay too.
 `value` = total packed trellis bytes / total time over the timed steps.
 `roofline` = the dominant GEMV (the K whose calls take the most time; one call = one
-gemv1_kernel<K> launch): algorithmic bytes per call (ic*oc*K/8) / its mean duration from
-HIP events recorded on the replay stream around a graph of the same steps, against
-8 TB/s.  `traffic` = HBM bytes per call measured with
+gemv1_kernel<K> launch and one gemv1_finish_kernel launch): algorithmic bytes per call
+(ic*oc*K/8) / its mean duration from HIP events recorded on the replay stream around a
+graph of the same steps, against 8 TB/s.  `traffic` = HBM bytes per call measured with
 rocprofv3 FETCH_SIZE + WRITE_SIZE and scaled by the same counters' reading for a plain
 copy of known size (profiles/gemv_traffic.json; `python bench.py --copy-calib` is the
 calibration workload).
@@ -667,7 +667,8 @@ def main():
                    "hbm_frac": round(r["value"] / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["frac"], 4), "traffic": traffic,
-                     "kernel": f"exl3_gemv K={r['dom']}: gemv1_kernel<{r['dom']}, 0, true, 1> (one launch per call)",
+                     "kernel": f"exl3_gemv K={r['dom']}: gemv1_kernel<{r['dom']}, 0, true, 1> + gemv1_finish_kernel<1, true> "
+                               "(one call = the decode launch and the launch that adds the split column groups)",
                      "bytes_per_launch": dom["bytes"], "mean_launch_us": round(dom["mean_us"], 3)},
         "per_K": {str(K): {"GB/s": round(v["gbs"], 1), "frac": round(v["frac"], 4),
                            "mean_us": round(v["mean_us"], 3)} for K, v in r["per_k"].items()},
