@@ -20,6 +20,8 @@ BUILD = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "orcasaq2", "libexl3hip.so")
 MEASURE = os.path.join(CSRC, "measure")
 CEILING = os.path.join(HERE, "orcasaq2", "libexl3ceiling.so")
+REPLAY_SRC = os.path.join(CSRC, "replay", "addr_replay.hip")
+REPLAY = os.path.join(HERE, "orcasaq2", "libexl3replay.so")
 ARCH = os.environ.get("EXL3_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -70,6 +72,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     subprocess.run(cmd, check=True)
     os.replace(tmp, OUT)
     build_ceiling(verbose)
+    build_replay(verbose)
     return OUT
 
 
@@ -88,6 +91,21 @@ def build_ceiling(verbose: bool = False) -> str:
         raise RuntimeError(f"hipcc failed for the measurement library:\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, CEILING)
     return CEILING
+
+
+def build_replay(verbose: bool = False) -> str:
+    """The CPU address replay of the GEMV and stream-K GEMM plans (csrc/replay): host code
+    only, checked by the CPU test suite.  Not part of libexl3hip or its C ABI."""
+    cc = hipcc()
+    tmp = REPLAY + ".tmp"
+    cmd = [cc] + HIPCC_FLAGS + ["-shared", "-o", tmp, REPLAY_SRC]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for the address replay:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, REPLAY)
+    return REPLAY
 
 
 if __name__ == "__main__":

@@ -27,73 +27,9 @@
 //   * LDS reads of 16 bytes feed the MFMAs.
 // Epilogue per 128-output block: rows through LDS, FWHT across a wave, * svh, fp16 store.
 #include "exl3_common.h"
-#include "exl3_launch.h"
+#include "gemm_sk_plan.h"
 
 namespace exl3 {
-
-constexpr int SK_WAVES = 8;
-constexpr int SK_BN = 256;
-constexpr int SK_KS = 64;                     // inputs per K-step (4 tile rows)
-constexpr int SK_LD = SK_KS + 8;              // halves per LDS row of the A and B tiles
-constexpr int SK_CLD = 128 + 4;               // floats per epilogue row in LDS (BM = 256)
-constexpr int SK_MAXSH = 8;                   // shards per launch
-constexpr int SK_PIPE16 = 24;                 // 16-row launches up to this many K-steps per CU: two buffers
-
-// Wave grid of a BM x 256 tile: WM x WN waves, each MB x NB blocks of 16 x 16.
-template <int BM>
-struct SkCfg;
-template <>
-struct SkCfg<256> { static constexpr int WM = 2, WN = 4, MB = 8, NB = 4; };
-template <>
-struct SkCfg<128> { static constexpr int WM = 1, WN = 8, MB = 8, NB = 2; };
-template <>
-struct SkCfg<64> { static constexpr int WM = 1, WN = 8, MB = 4, NB = 2; };
-template <>
-struct SkCfg<96> { static constexpr int WM = 1, WN = 8, MB = 6, NB = 2; };
-template <>
-struct SkCfg<48> { static constexpr int WM = 1, WN = 8, MB = 3, NB = 2; };
-template <>
-struct SkCfg<32> { static constexpr int WM = 1, WN = 8, MB = 2, NB = 2; };
-template <>
-struct SkCfg<16> { static constexpr int WM = 1, WN = 8, MB = 1, NB = 2; };
-
-template <int BM>
-constexpr int sk_acc() { return SkCfg<BM>::MB * SkCfg<BM>::NB * 4; }   // fp32 accumulators per lane
-// LDS of a launch: the A and B tiles of one K-step, twice for BM >= 32 (the tiles of step
-// s + 1 are written while the MFMAs read those of step s; one workgroup per CU), once for
-// BM = 16 (three workgroups per CU overlap one another's phases instead).  Measured on
-// MI355X at 17..64 rows: the two-buffer pipeline with one workgroup per CU beats one buffer
-// with two workgroups per CU by 28% on 17408 -> 5120 and 6% on 5120 -> 17408.
-// A 16-row launch takes either form (NBUF = 1 or 2, chosen by its length).
-template <int BM>
-constexpr int sk_nbuf() { return BM >= 32 ? 2 : 1; }
-// Waves per SIMD the register budget is set for, and workgroups per CU of a launch.
-template <int BM, int NBUF>
-constexpr int sk_wpe() { return NBUF == 2 ? 2 : 6; }
-template <int BM, int NBUF>
-constexpr int sk_wgpc() { return NBUF == 2 ? 1 : 3; }
-template <int BM>
-constexpr int sk_buf() { return (BM + SK_BN) * SK_LD; }                   // halves per A + B buffer
-template <int BM, int NBUF>
-constexpr int sk_lds() { return NBUF * sk_buf<BM>() * 2; }      // bytes
-
-struct SkShard {
-    const uint16_t* Ah;        // (rows, ic) fp16, fp16(H(A * suh)) of this shard
-    const uint32_t* trellis;   // (ic/16, oc/16, 8K) u32
-    const uint16_t* svh;       // (oc)
-    uint16_t* C;               // (rows, ldc) fp16, columns [0, oc)
-    long ldc;
-    int oc, ntn, tbeg;         // outputs, 256-wide tile columns, first tile of the shard
-    int K;                     // bits per weight (read by the per-shard-K kernel)
-};
-
-struct SkArgs {
-    uint32_t* counters;        // one per tile, zeroed by sk_clear_kernel before the launch
-    float* slots;              // (tiles + G) x SK_WAVES x acc x 64 fp32
-    int rows, ic, nks, ntiles, nshards;
-    int q, r;                  // K-steps per workgroup: q + (g < r)
-    SkShard sh[SK_MAXSH];
-};
 
 __global__ void sk_clear_kernel(uint32_t* counters, int n)
 {
@@ -101,27 +37,17 @@ __global__ void sk_clear_kernel(uint32_t* counters, int n)
     if (i < n) counters[i] = 0u;
 }
 
-// Set-up of a grouped launch in one kernel: the tile counters to zero and, for every
-// shard, its activations Ah = fp16(H128(A * suh)) (rows x ic), one wave per (shard, row,
-// 128-input block).
-struct SkPrepArgs {
-    const uint16_t* A;
-    int rows, ic, nsh, nblk;
-    const uint16_t* suh[SK_MAXSH];
-    uint16_t* Ah[SK_MAXSH];
-    uint32_t* counters;
-    int ntiles;
-};
-
+// Set-up of a grouped launch (SkPrepArgs): the tile counters to zero and, for every shard,
+// its activations Ah = fp16(H128(A * suh)), one wave per (shard, row, 128-input block).
 __global__ __launch_bounds__(256) void sk_prep_kernel(const SkPrepArgs a)
 {
     const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (w < a.ntiles && lane == 0) a.counters[w] = 0u;
     if (w >= a.nsh * a.rows * a.nblk) return;   // whole waves only
-    const int b = w % a.nblk, rs = w / a.nblk;
-    const int r = rs % a.rows, s = rs / a.rows;
-    const long off = (long)r * a.ic + b * 128;
+    int s, r, b;
+    sk_prep_wave(a, w, s, r, b);
+    const long off = sk_prep_elem(a, r, b);
     const uint32_t xw = reinterpret_cast<const uint32_t*>(a.A + off)[lane];
     const uint32_t sw = reinterpret_cast<const uint32_t*>(a.suh[s] + b * 128)[lane];
     float v0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(xw & 0xffffu)) *
@@ -131,24 +57,6 @@ __global__ __launch_bounds__(256) void sk_prep_kernel(const SkPrepArgs a)
     wave_fwht128(v0, v1);
     reinterpret_cast<uint32_t*>(a.Ah[s] + off)[lane] =
         (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) | ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
-}
-
-// Logical workgroup of launch slot b.  Launch slots go to the 8 XCDs round-robin (slot b on
-// XCD b % 8), so when G is a multiple of 8 each XCD gets a contiguous block of logical
-// workgroups -- for a 256-row GEMM, the tiles of one row block: their A rows are shared
-// in that XCD's L2.  Any placement gives the same results; this one only saves traffic.
-__device__ __forceinline__ int sk_logical(int b)
-{
-    const int G = gridDim.x;
-    return (G & 7) ? b : (b & 7) * (G >> 3) + (b >> 3);
-}
-
-// First K-step (global numbering) of workgroup g, and the workgroup holding K-step u.
-__device__ __forceinline__ long sk_first(const SkArgs& a, int g) { return (long)g * a.q + min(g, a.r); }
-__device__ __forceinline__ int sk_wg_of(const SkArgs& a, long u)
-{
-    const long big = (long)a.r * (a.q + 1);
-    return u < big ? (int)(u / (a.q + 1)) : a.r + (int)((u - big) / a.q);
 }
 
 // (w_a, w_b) packed: each weight is the fp16 sum of its masked word's two halves (one RNE
@@ -225,12 +133,12 @@ __global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(s
 void gemm_sk_kernel(const SkArgs a)
 {
     using Cfg = SkCfg<BM>;
-    constexpr int MB = Cfg::MB, NB = Cfg::NB, ACC = sk_acc<BM>();
+    constexpr int MB = Cfg::MB, NB = Cfg::NB;
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-    auto As = [&](int b) { return reinterpret_cast<_Float16*>(lds) + b * sk_buf<BM>(); };
-    auto Bs = [&](int b) { return reinterpret_cast<_Float16*>(lds) + b * sk_buf<BM>() + BM * SK_LD; };
+    auto As = [&](int b) { return reinterpret_cast<_Float16*>(lds) + sk_as<BM>(b); };
+    auto Bs = [&](int b) { return reinterpret_cast<_Float16*>(lds) + sk_bs<BM>(b); };
 
-    const int g = sk_logical(blockIdx.x);
+    const int g = sk_logical(blockIdx.x, gridDim.x);
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int lane = tid & 63;
@@ -238,15 +146,13 @@ void gemm_sk_kernel(const SkArgs a)
     const Dot2Consts kc = dot2_consts();
 
     // A-tile loader: thread t moves 16 bytes of row t / 8 (+ 64 p), segment t % 8.
-    const int arow = tid >> 3, aseg = tid & 7;
+    const int arow = sk_arow(tid), aseg = sk_aseg(tid);
     constexpr int AP = (BM + 63) / 64;               // passes; pass p moves rows 64 p + arow < BM
-    auto aload = [&](int p) { return 64 * p + arow < BM; };
-    // B chunk of this thread: chunk id tid = 8 * tile + c, tile = 16 ti_l + tn_l (a tile's
-    // 8 chunks on 8 consecutive lanes)
+    auto aload = [&](int p) { return sk_apass<BM>(p, arow); };
+    // B chunk of this thread (sk_b_word): a tile's 8 chunks on 8 consecutive lanes
     const int c = lane & 7;
     const bool first_lane = c == 0;
-    const int btile = tid >> 3;
-    const int bn0 = 16 * (btile & 15) + c, bk0 = 16 * (btile >> 4);
+    const int bn0 = sk_bn0(tid), bk0 = sk_bk0(tid);
 
     f32x4 acc[MB][NB];
     uint4 areg[AP];
@@ -254,19 +160,12 @@ void gemm_sk_kernel(const SkArgs a)
     const long u_begin = sk_first(a, g), u_end = sk_first(a, g + 1);
     long u = u_begin;
     while (u < u_end) {
-        const int t = (int)(u / a.nks);
-        const int s0 = (int)(u - (long)t * a.nks);
-        const int s1 = (int)min((long)a.nks, s0 + (u_end - u));
-        int si = 0;
-#pragma unroll
-        for (int i = 1; i < SK_MAXSH; i++)
-            if (i < a.nshards && t >= a.sh[i].tbeg) si = i;
-        const SkShard& S = a.sh[si];
-        const int tl = t - S.tbeg;
-        const int tm = tl / S.ntn, tn = tl - tm * S.ntn;
-        const int m0 = tm * BM;
-        const int tc = S.oc >> 4;                    // tile columns of W_q
-        const int btn = 16 * tn + (btile & 15);
+        const SkPiece pc = sk_piece<BM>(a, u, u_end);
+        const int t = pc.t, s0 = pc.s0, s1 = pc.s1;
+        const SkShard& S = a.sh[pc.si];
+        const int tn = pc.tn, m0 = pc.m0;
+        const int tc = pc.tc;                        // tile columns of W_q
+        const int btn = sk_btn(tid, tn);
         const bool bok = btn < tc;
 
 #pragma unroll
@@ -282,11 +181,10 @@ void gemm_sk_kernel(const SkArgs a)
                 for (int p = 0; p < AP; p++) {
                     const int row = m0 + 64 * p + arow;
                     areg[p] = (aload(p) && row < a.rows)
-                        ? *reinterpret_cast<const uint4*>(S.Ah + (long)row * a.ic + s * SK_KS + aseg * 8)
+                        ? *reinterpret_cast<const uint4*>(S.Ah + sk_a_elem(a, row, s, aseg))
                         : uint4{0u, 0u, 0u, 0u};
                 }
-                const int ti = 4 * s + (btile >> 4);
-                sk_load<KK>(w, S.trellis + ((long)ti * tc + (bok ? btn : 0)) * (8 * KK) + c * KK, bok);
+                sk_load<KK>(w, S.trellis + sk_b_word(sk_bti(tid, s), tc, sk_bcol(btn, tc), c, KK), bok);
             };
             // the registers of a K-step into LDS buffer b: A as loaded, B decoded
             auto store_step = [&](int b) {
@@ -294,14 +192,12 @@ void gemm_sk_kernel(const SkArgs a)
                 _Float16* bs = Bs(b);
 #pragma unroll
                 for (int p = 0; p < AP; p++)
-                    if (aload(p)) *reinterpret_cast<uint4*>(as + (64 * p + arow) * SK_LD + aseg * 8) = areg[p];
+                    if (aload(p)) *reinterpret_cast<uint4*>(as + sk_a_store(p, arow, aseg)) = areg[p];
                 chunk_prev_dpp<KK>(w, first_lane);
                 uint4 o[4];
                 sk_decode<KK, CB>(w, kc, o);
-                *reinterpret_cast<uint4*>(bs + bn0 * SK_LD + bk0) = o[0];
-                *reinterpret_cast<uint4*>(bs + bn0 * SK_LD + bk0 + 8) = o[1];
-                *reinterpret_cast<uint4*>(bs + (bn0 + 8) * SK_LD + bk0) = o[2];
-                *reinterpret_cast<uint4*>(bs + (bn0 + 8) * SK_LD + bk0 + 8) = o[3];
+#pragma unroll
+                for (int j = 0; j < 4; j++) *reinterpret_cast<uint4*>(bs + sk_b_store(bn0, bk0, j)) = o[j];
             };
             // the MFMAs of one K-step from LDS buffer b
             auto mfma_step = [&](int b) {
@@ -312,12 +208,10 @@ void gemm_sk_kernel(const SkArgs a)
                     f16x8 bf[NB];
 #pragma unroll
                     for (int nb = 0; nb < NB; nb++)
-                        bf[nb] = *reinterpret_cast<const f16x8*>(bs + (NB * 16 * wn + 16 * nb + (lane & 15)) * SK_LD +
-                                                                 32 * h + 8 * (lane >> 4));
+                        bf[nb] = *reinterpret_cast<const f16x8*>(bs + sk_b_frag<BM>(wn, nb, lane, h));
 #pragma unroll
                     for (int mb = 0; mb < MB; mb++) {
-                        const f16x8 af = *reinterpret_cast<const f16x8*>(as + (MB * 16 * wm + 16 * mb + (lane & 15)) * SK_LD +
-                                                                         32 * h + 8 * (lane >> 4));
+                        const f16x8 af = *reinterpret_cast<const f16x8*>(as + sk_a_frag<BM>(wm, mb, lane, h));
 #pragma unroll
                         for (int nb = 0; nb < NB; nb++) acc[mb][nb] = mfma16x16x32(af, bf[nb], acc[mb][nb]);
                     }
@@ -383,7 +277,7 @@ void gemm_sk_kernel(const SkArgs a)
         bool finish = s0 == 0 && s1 == a.nks;
         if (!finish) {
             const int g_lo = sk_wg_of(a, (long)t * a.nks), g_hi = sk_wg_of(a, (long)(t + 1) * a.nks - 1);
-            uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + ((long)(t + g) * SK_WAVES + wave) * ACC * 64) + lane;
+            uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + sk_slot<BM>(t, g, wave)) + lane;
 #pragma unroll
             for (int mb = 0; mb < MB; mb++)
 #pragma unroll
@@ -417,7 +311,7 @@ void gemm_sk_kernel(const SkArgs a)
                 constexpr int RB = NP < 16 ? NP : 16;
                 for (int gg = g_lo; gg <= g_hi; gg++) {
                     const uint64_t* sl =
-                        reinterpret_cast<const uint64_t*>(a.slots + ((long)(t + gg) * SK_WAVES + wave) * ACC * 64) + lane;
+                        reinterpret_cast<const uint64_t*>(a.slots + sk_slot<BM>(t, gg, wave)) + lane;
 #pragma unroll
                     for (int b0 = 0; b0 < NP; b0 += RB) {
                         uint64_t v[RB];
@@ -461,25 +355,24 @@ void gemm_sk_kernel(const SkArgs a)
                 // and row half), then wave (wn & 1) transforms rows 8 (wn & 1) .. + 7.
                 const int blk = wn >> 1, half = wn & 1;
                 const uint32_t sv = load_sv(16 * tn + 8 * blk);
-                float* cs = reinterpret_cast<float*>(lds) + (wm * 2 + blk) * 16 * SK_CLD;
+                float* cs = reinterpret_cast<float*>(lds) + sk_c256(wm, blk, 0, 0);
 #pragma unroll
                 for (int mb = 0; mb < MB; mb++) {
 #pragma unroll
                     for (int nb = 0; nb < NB; nb++)
 #pragma unroll
                         for (int e = 0; e < 4; e++)
-                            cs[(4 * (lane >> 4) + e) * SK_CLD + 64 * half + 16 * nb + (lane & 15)] = acc[mb][nb][e];
+                            cs[sk_c256(0, 0, 4 * (lane >> 4) + e, 64 * half + 16 * nb + (lane & 15))] = acc[mb][nb][e];
                     __syncthreads();
 #pragma unroll
                     for (int r = 8 * half; r < 8 * half + 8; r++)   // eight independent transforms
-                        store_row(m0 + 128 * wm + 16 * mb + r, 16 * tn + 8 * blk, sv, cs[r * SK_CLD + 2 * lane],
-                                  cs[r * SK_CLD + 2 * lane + 1]);
+                        store_row(m0 + 128 * wm + 16 * mb + r, 16 * tn + 8 * blk, sv, cs[sk_c256(0, 0, r, 2 * lane)],
+                                  cs[sk_c256(0, 0, r, 2 * lane + 1)]);
                     __syncthreads();
                 }
             } else {
                 // 16 rows at a time through LDS (16 rows of 260 floats); wave w transforms the
                 // chunk's (row, block) pairs w, w + 8, w + 16, w + 24
-                constexpr int LD = SK_BN + 4;
                 float* cs = reinterpret_cast<float*>(lds);
                 const uint32_t sv[2] = {load_sv(16 * tn), load_sv(16 * tn + 8)};
 #pragma unroll
@@ -488,14 +381,14 @@ void gemm_sk_kernel(const SkArgs a)
                     for (int nb = 0; nb < NB; nb++)
 #pragma unroll
                         for (int e = 0; e < 4; e++)
-                            cs[(4 * (lane >> 4) + e) * LD + NB * 16 * wn + 16 * nb + (lane & 15)] = acc[mb][nb][e];
+                            cs[sk_cx(4 * (lane >> 4) + e, NB * 16 * wn + 16 * nb + (lane & 15))] = acc[mb][nb][e];
                     __syncthreads();
 #pragma unroll
                     for (int jj = 0; jj < 4; jj++) {
                         const int j = wave + SK_WAVES * jj;
                         const int r = j & 15, blk = j >> 4;
-                        store_row(m0 + 16 * mb + r, 16 * tn + 8 * blk, sv[blk], cs[r * LD + 128 * blk + 2 * lane],
-                                  cs[r * LD + 128 * blk + 2 * lane + 1]);
+                        store_row(m0 + 16 * mb + r, 16 * tn + 8 * blk, sv[blk], cs[sk_cx(r, 128 * blk + 2 * lane)],
+                                  cs[sk_cx(r, 128 * blk + 2 * lane + 1)]);
                     }
                     if (mb + 1 < MB) __syncthreads();
                 }
@@ -507,8 +400,6 @@ void gemm_sk_kernel(const SkArgs a)
 
 // ---------------------------------------------------------------- host side
 
-static inline size_t sk_align(size_t x) { return (x + 255) & ~(size_t)255; }
-
 int gemm_sk_cus()
 {
     int dev = 0, cus = 0;
@@ -517,71 +408,17 @@ int gemm_sk_cus()
     return cus;
 }
 
-// Workgroups per launch: sk_wgpc per CU, all resident at once.
-template <int BM, int NBUF = sk_nbuf<BM>()>
-static int sk_gmax() { return sk_wgpc<BM, NBUF>() * gemm_sk_cus(); }
+size_t gemm_sk_slot_bytes(int rows, int oc) { return sk_single_bytes(rows, oc, gemm_sk_cus()); }
 
-template <int BM>
-static size_t sk_slot() { return (size_t)SK_WAVES * sk_acc<BM>() * 64 * sizeof(float); }
+size_t gemv_sk_bytes(int rows, int ic, int oc) { return sk_grouped_bytes<16>(rows, ic, oc, gemm_sk_cus()); }
 
-static int sk_ntn(int oc) { return (oc + SK_BN - 1) / SK_BN; }
-
-// Counters and slots of one launch of `tiles` tiles and up to G workgroups.
-template <int BM>
-static size_t sk_ws(long tiles, int G) { return sk_align((size_t)tiles * 4) + (size_t)(tiles + G) * sk_slot<BM>(); }
-
-// Tile height of a prefill launch of `rows` rows.  Each weight is decoded once per row tile;
-// a taller tile pays that decode over more rows but MFMA work for padding rows and bigger
-// partial sums.  Measured on MI355X (17408 -> 5120, 5120 -> 17408, 5120 -> 6144): 32 is
-// fastest up to 32 rows (13-22% below 64-row tiles), 48 up to 48 (8-15% below), 64 up to
-// 64, 96 up to 96 (4-9% below 128-row tiles), 128 up to 384 (two or
-// three 128-row tiles beat one 256-row tile: more tiles, fewer stream-K partial sums per
-// tile), 256 above.
-static int gemm_sk_bm(int rows)
+size_t gemm_grouped_shard_bytes(int rows, int ic, int oc)
 {
-#ifdef EXL3_SK_FORCE_BM
-    return EXL3_SK_FORCE_BM;
-#else
-    return rows <= 32 ? 32 : rows <= 48 ? 48 : rows <= 64 ? 64 : rows <= 96 ? 96 : rows <= 384 ? 128 : 256;
-#endif
+    return sk_grouped_bytes_bm(gemm_sk_bm(rows), rows, ic, oc, gemm_sk_cus());
 }
-
-template <int BM>
-static size_t gemm_sk_ws(int rows, int oc)
-{
-    return sk_ws<BM>((long)((rows + BM - 1) / BM) * sk_ntn(oc), sk_gmax<BM>());
-}
-
-size_t gemm_sk_slot_bytes(int rows, int oc)
-{
-    switch (gemm_sk_bm(rows)) {
-    case 32: return gemm_sk_ws<32>(rows, oc);
-    case 48: return gemm_sk_ws<48>(rows, oc);
-    case 96: return gemm_sk_ws<96>(rows, oc);
-    case 64: return gemm_sk_ws<64>(rows, oc);
-    case 128: return gemm_sk_ws<128>(rows, oc);
-    default: return gemm_sk_ws<256>(rows, oc);
-    }
-}
-
-// Per-shard workspace of a grouped launch (several shards reading the same A): the shard's
-// activations fp16(H(A * suh)), then its share of counters and slots (each launch has at
-// least one shard, so the shares cover it).
-template <int BM>
-static size_t sk_grouped_bytes(int rows, int ic, int oc)
-{
-    return sk_align((size_t)rows * ic * 2) + sk_ws<BM>((long)((rows + BM - 1) / BM) * sk_ntn(oc), sk_gmax<BM>());
-}
-
-size_t gemv_sk_bytes(int rows, int ic, int oc) { return sk_grouped_bytes<16>(rows, ic, oc); }
 
 template <int K, int CB, int BM, int NBUF>
 static const void* sk_fn() { return reinterpret_cast<const void*>(&gemm_sk_kernel<K, CB, BM, NBUF>); }
-
-// The per-piece-K kernel (K = 0) exists for BM <= 128; a mixed-K group of 256-row tiles
-// is launched once per K instead.
-template <int BM>
-constexpr bool sk_has_k0() { return BM <= 128; }
 
 template <int BM, int NBUF>
 static const void* sk_fn_kcb(int K, int cb)
@@ -597,144 +434,73 @@ static const void* sk_fn_kcb(int K, int cb)
     return nullptr;
 }
 
-// One stream-K launch over a.sh[0 .. nshards): clears its tile counters, then runs.  `ws`
-// holds the counters and slots (sk_ws bytes).
-template <int BM, int NBUF = sk_nbuf<BM>()>
-static int sk_launch(SkArgs& a, int K, int cb, char* ws, size_t ws_bytes, const char* what, hipStream_t stream,
-                     bool clear = true)
+static const void* sk_fn_any(int BM, int NBUF, int K, int cb)
 {
-    const long units = (long)a.ntiles * a.nks;
-    // at least 8 K-steps per workgroup: a tile has at most nks / 8 + 2 contributors
-    int G = (int)std::min<long>(sk_gmax<BM, NBUF>(), std::max<long>(1, units / 8));
-    const size_t cbytes = sk_align((size_t)a.ntiles * 4);
-    const long fit = ws_bytes > cbytes ? (long)((ws_bytes - cbytes) / sk_slot<BM>()) - a.ntiles : 0;
-    if (fit < 1)
-        return set_error(EXL3_ERR_WORKSPACE, "%s: workspace of %zu bytes, %zu needed", what, ws_bytes,
-                         sk_ws<BM>(a.ntiles, G));
-    if (G > fit) G = (int)fit;   // a workspace sized on a device with fewer CUs
-    a.q = (int)(units / G);
-    a.r = (int)(units % G);
-    a.counters = reinterpret_cast<uint32_t*>(ws);
-    a.slots = reinterpret_cast<float*>(ws + cbytes);
-    if (clear) {
+    switch (BM) {
+    case 16: return NBUF == 2 ? sk_fn_kcb<16, 2>(K, cb) : sk_fn_kcb<16, 1>(K, cb);
+    case 32: return sk_fn_kcb<32, 2>(K, cb);
+    case 48: return sk_fn_kcb<48, 2>(K, cb);
+    case 64: return sk_fn_kcb<64, 2>(K, cb);
+    case 96: return sk_fn_kcb<96, 2>(K, cb);
+    case 128: return sk_fn_kcb<128, 2>(K, cb);
+    case 256: return sk_fn_kcb<256, 2>(K, cb);
+    }
+    return nullptr;
+}
+
+static int sk_lds_any(int BM, int NBUF)
+{
+    switch (BM) {
+    case 16: return NBUF == 2 ? sk_lds<16, 2>() : sk_lds<16, 1>();
+    case 32: return sk_lds<32, 2>();
+    case 48: return sk_lds<48, 2>();
+    case 64: return sk_lds<64, 2>();
+    case 96: return sk_lds<96, 2>();
+    case 128: return sk_lds<128, 2>();
+    default: return sk_lds<256, 2>();
+    }
+}
+
+// The kernels of one planned launch: the counter clear or the set-up kernel, then the
+// stream-K kernel.
+static int sk_emit(const SkLaunch& L, const char* what, hipStream_t stream)
+{
+    SkArgs a = *L.args;
+    if (L.clear) {
         hipLaunchKernelGGL(sk_clear_kernel, dim3((a.ntiles + 255) / 256), dim3(256), 0, stream, a.counters, a.ntiles);
         const int rc = check_launch(what);
         if (rc != EXL3_OK) return rc;
     }
-    const void* fn = sk_fn_kcb<BM, NBUF>(K, cb);
-    if (!fn) return set_error(EXL3_ERR_ARG, "%s: K=%d is not in 1..8", what, K);   // K = 0: per shard
-    if (sk_lds<BM, NBUF>() > 64 * 1024) {
-        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, sk_lds<BM, NBUF>());
+    if (L.prep) {
+        hipLaunchKernelGGL(sk_prep_kernel, dim3((unsigned)((L.prep_waves + 3) / 4)), dim3(256), 0, stream, *L.prep_args);
+        const int rc = check_launch(what);
+        if (rc != EXL3_OK) return rc;
+    }
+    const void* fn = sk_fn_any(L.BM, L.NBUF, L.K, L.cb);
+    if (!fn) return set_error(EXL3_ERR_ARG, "%s: K=%d is not in 1..8", what, L.K);   // K = 0: per shard
+    const int lds = sk_lds_any(L.BM, L.NBUF);
+    if (lds > 64 * 1024) {
+        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         (void)hipGetLastError();
     }
     void* kargs[] = {&a};
-    hipLaunchKernel(fn, dim3(G), dim3(64 * SK_WAVES), kargs, sk_lds<BM, NBUF>(), stream);
+    hipLaunchKernel(fn, dim3(L.G), dim3(64 * SK_WAVES), kargs, lds, stream);
     return check_launch(what);
 }
 
 int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
                      size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream)
 {
-    SkArgs a = {};
-    a.rows = rows;
-    a.ic = ic;
-    a.nks = ic / SK_KS;
-    a.nshards = 1;
-    SkShard& s = a.sh[0];
-    s.Ah = Ah;
-    s.trellis = trellis;
-    s.svh = svh;
-    s.C = C;
-    s.ldc = oc;
-    s.oc = oc;
-    s.ntn = sk_ntn(oc);
-    s.tbeg = 0;
-    s.K = K;
-    const int bm = gemm_sk_bm(rows);
-    a.ntiles = ((rows + bm - 1) / bm) * s.ntn;
-    switch (bm) {
-    case 32: return sk_launch<32>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
-    case 48: return sk_launch<48>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
-    case 96: return sk_launch<96>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
-    case 64: return sk_launch<64>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
-    case 128: return sk_launch<128>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
-    default: return sk_launch<256>(a, K, cb, ws, ws_bytes, "exl3_gemm (stream-K)", stream);
-    }
+    return sk_plan_single(Ah, trellis, C, svh, ws, ws_bytes, rows, ic, oc, K, cb, gemm_sk_cus(),
+                          [&](const SkLaunch& L) { return sk_emit(L, "exl3_gemm (stream-K)", stream); });
 }
 
-// Shards that read the same A (rows x ic): per codebook (and per K where no per-piece-K
-// kernel exists), groups of up to SK_MAXSH shards; per group one set-up kernel (the
-// shards' activations, the group's tile counters) and one stream-K launch -- a single-K
-// kernel when the group's shards share K, else the per-shard-K one.
 template <int BM>
 static int sk_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws,
                                size_t ws_bytes, const char* what, hipStream_t stream)
 {
-    const int ic = shards[0].ic;
-    const int nrb = (rows + BM - 1) / BM;
-    bool done[EXL3_MAX_SHARDS] = {false};
-    size_t off = 0;
-    const size_t ah = sk_align((size_t)rows * ic * 2);
-    for (int i = 0; i < nshards; i++) {
-        if (done[i]) continue;
-        SkArgs a = {};
-        SkPrepArgs p = {};
-        a.rows = p.rows = rows;
-        a.ic = p.ic = ic;
-        a.nks = ic / SK_KS;
-        p.A = A;
-        p.nblk = ic / 128;
-        int tiles = 0, K = shards[i].K;
-        for (int s = i; s < nshards && a.nshards < SK_MAXSH; s++) {
-            if (done[s] || shards[s].cb != shards[i].cb) continue;
-            if (!sk_has_k0<BM>() && shards[s].K != shards[i].K) continue;
-            const GemvShard& d = shards[s];
-            if (d.K < 1 || d.K > 8) return set_error(EXL3_ERR_ARG, "%s: K=%d is not in 1..8", what, d.K);
-            if (off + ah > ws_bytes)
-                return set_error(EXL3_ERR_WORKSPACE, "%s: workspace of %zu bytes is too small", what, ws_bytes);
-            uint16_t* Ah = reinterpret_cast<uint16_t*>(ws + off);
-            off += ah;
-            p.suh[a.nshards] = d.suh;
-            p.Ah[a.nshards] = Ah;
-            SkShard& e = a.sh[a.nshards++];
-            e.Ah = Ah;
-            e.trellis = d.trellis;
-            e.svh = d.svh;
-            e.C = d.C;
-            e.ldc = d.ldc;
-            e.oc = d.oc;
-            e.ntn = sk_ntn(d.oc);
-            e.tbeg = tiles;
-            e.K = d.K;
-            if (d.K != K) K = 0;
-            tiles += nrb * e.ntn;
-            done[s] = true;
-        }
-        a.ntiles = p.ntiles = tiles;
-        p.nsh = a.nshards;
-        p.counters = reinterpret_cast<uint32_t*>(ws + off);
-        const long waves = std::max<long>((long)p.nsh * rows * p.nblk, tiles);
-        hipLaunchKernelGGL(sk_prep_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, p);
-        int rc = check_launch(what);
-        if (rc != EXL3_OK) return rc;
-        const size_t need = sk_ws<BM>(tiles, sk_gmax<BM>());
-        const size_t avail = ws_bytes > off ? ws_bytes - off : 0;
-        // 16-row tiles: a short launch (at most SK_PIPE16 K-steps per CU) takes the two-buffer
-        // pipeline with one workgroup per CU, a longer one three single-buffer workgroups
-        // per CU (measured on MI355X at 16 rows: qkv, ~10 K-steps per CU, 31 -> 26 us;
-        // gate_up, ~42 per CU, 56 -> 62 us with two buffers)
-        if constexpr (BM == 16) {
-            if ((long)tiles * a.nks <= (long)SK_PIPE16 * gemm_sk_cus())
-                rc = sk_launch<16, 2>(a, K, shards[i].cb, ws + off, std::min(need, avail), what, stream, false);
-            else
-                rc = sk_launch<16, 1>(a, K, shards[i].cb, ws + off, std::min(need, avail), what, stream, false);
-        } else {
-            rc = sk_launch<BM>(a, K, shards[i].cb, ws + off, std::min(need, avail), what, stream, false);
-        }
-        if (rc != EXL3_OK) return rc;
-        off += std::min(need, avail);
-    }
-    return EXL3_OK;
+    return sk_plan_grouped<BM>(A, shards, nshards, rows, ws, ws_bytes, what, gemm_sk_cus(),
+                               [&](const SkLaunch& L) { return sk_emit(L, what, stream); });
 }
 
 // 2..16 rows: 16-row tiles.
@@ -745,18 +511,6 @@ int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, in
 }
 
 // Prefill of several shards (exl3_gemm_grouped): tile height by rows, as for one shard.
-size_t gemm_grouped_shard_bytes(int rows, int ic, int oc)
-{
-    switch (gemm_sk_bm(rows)) {
-    case 32: return sk_grouped_bytes<32>(rows, ic, oc);
-    case 48: return sk_grouped_bytes<48>(rows, ic, oc);
-    case 96: return sk_grouped_bytes<96>(rows, ic, oc);
-    case 64: return sk_grouped_bytes<64>(rows, ic, oc);
-    case 128: return sk_grouped_bytes<128>(rows, ic, oc);
-    default: return sk_grouped_bytes<256>(rows, ic, oc);
-    }
-}
-
 int gemm_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws,
                           size_t ws_bytes, hipStream_t stream)
 {

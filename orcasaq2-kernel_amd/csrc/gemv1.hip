@@ -37,114 +37,9 @@
 //      inside the launch (measured on MI355X against a last-arriving-workgroup finish with
 //      agent-scope stores and a counter: 4-9% faster on every 27B projection shape).
 #include "exl3_common.h"
-#include "exl3_launch.h"
+#include "gemv1_plan.h"
 
 namespace exl3 {
-
-constexpr int G1_NW = 8;                 // waves per workgroup
-constexpr int G1_MAXSH = 8;              // shards per launch
-constexpr int G1_WG_PER_CU = 4;          // target resident workgroups per CU (8 waves / SIMD)
-constexpr int G1_GMAX = 2048;            // workgroups per launch (bounds the slot area)
-
-// Units a wave keeps in flight: one.  Eight waves per SIMD already keep enough loads in
-// flight, and every unit more per wave lengthens the memory queues that a launch's first
-// units and activation loads wait behind: measured on MI355X (down_proj, per call), depth 1
-// against 2 and against 24 / (K + 3) clamped to 2..6: K = 2 18.6 / 18.7 / 19.6 us, K = 3
-// 18.9 / 19.6 / 20.9, K = 4 19.4 / 19.8 / 20.7, K = 5 19.4 / 20.4 / 21.4.
-constexpr int g1_depth(int) { return 1; }
-
-struct G1Shard {
-    const uint32_t* trellis;   // (ic/16, oc/16, 8K) u32
-    const uint16_t* suh;       // (ic)
-    const uint16_t* svh;       // (oc)
-    uint16_t* C;               // (nrows, ldc) fp16 output, columns [0, oc)
-    long ldc;
-    int ubeg;                  // first unit of the shard
-    int sbeg;                  // first segment of the shard
-    int oc16;                  // tile columns
-    int ncg;                   // column groups (oc / 128)
-};
-
-// Division by a launch constant d >= 2 of any x < 2^31 without a division routine (the
-// scalar unit is shared by every wave of a CU, and a 64-bit division is ~130 of its
-// instructions): floor(x / d) = floor(x * m / 2^(31 + l)), l = ceil(log2 d),
-// m = floor(2^(31 + l) / d) + 1 < 2^32 (Granlund and Montgomery, PLDI 1994, Thm 4.2 with
-// N = 31).
-struct G1Div {
-    uint32_t m;
-    int sh;                    // l - 1
-};
-
-__device__ __forceinline__ int g1_div(int x, G1Div d)
-{
-    return (int)(__umulhi((uint32_t)x, d.m) >> d.sh);
-}
-
-// One group of shards with the same K and codebook, decoded by G workgroups.
-struct G1Group {
-    const uint16_t* x;         // (nrows, ic) fp16
-    int nrows;                 // activation rows, 1 .. R of the kernel
-    float* slots;              // (G + segments) x R x 128 fp32 partials of split segments
-    int U, G, ntr, nshards, nsegs;
-    int q, r;                  // U = q G + r: workgroup g owns q + (g < r) units
-    G1Div dntr, dq, dq1;       // division by ntr, q, q + 1
-};
-
-// A launch of one group (shards 0 .. nshards - 1 of the table).
-struct G1Args {
-    G1Group grp;
-    G1Shard sh[G1_MAXSH];
-};
-
-// A launch of several groups of one codebook, one K each: group i owns workgroups
-// gbeg[i] .. gbeg[i + 1] - 1 and shards sh0[i] .. sh0[i] + grp[i].nshards - 1; in the finish
-// kernel it owns blocks fbeg[i] .. fbeg[i] + grp[i].nsegs - 1 (one per segment).
-struct G1Multi {
-    G1Group grp[G1_MAXSH];
-    G1Shard sh[G1_MAXSH];
-    int gbeg[G1_MAXSH], sh0[G1_MAXSH], K[G1_MAXSH], fbeg[G1_MAXSH];
-    int ngrp;
-};
-
-// First unit of workgroup g: the first r workgroups own q + 1 units, the others q.
-__device__ __forceinline__ int g1_first_unit(const G1Group& a, int g)
-{
-    return g * a.q + min(g, a.r);
-}
-
-// Workgroup whose unit range holds unit u.
-__device__ __forceinline__ int g1_wg_of(const G1Group& a, int u)
-{
-    const int big = a.r * (a.q + 1);
-    return u < big ? g1_div(u, a.dq1) : a.r + g1_div(u - big, a.dq);
-}
-
-// Shard holding segment S / unit u.  Every table entry is read at a constant offset, so the
-// scalar loads of the whole table issue together instead of as a chain of dependent loads
-// (each a few hundred cycles); a single-shard launch (ONE) reads nothing.
-template <bool ONE>
-__device__ __forceinline__ int g1_shard_of_seg(const G1Group& a, const G1Shard* sht, int S)
-{
-    int s = 0;
-    if constexpr (!ONE) {
-#pragma unroll
-        for (int i = 1; i < G1_MAXSH; i++)
-            if (i < a.nshards && S >= sht[i].sbeg) s = i;
-    }
-    return s;
-}
-
-template <bool ONE>
-__device__ __forceinline__ int g1_shard_of_unit(const G1Group& a, const G1Shard* sht, int u)
-{
-    int s = 0;
-    if constexpr (!ONE) {
-#pragma unroll
-        for (int i = 1; i < G1_MAXSH; i++)
-            if (i < a.nshards && u >= sht[i].ubeg) s = i;
-    }
-    return s;
-}
 
 __device__ __forceinline__ float g1_lo(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v & 0xffffu)); }
 __device__ __forceinline__ float g1_hi(uint32_t v) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(v >> 16)); }
@@ -222,61 +117,25 @@ __device__ __forceinline__ uint32_t g1_dup(float v)
 
 // ---------------------------------------------------------------- decode kernel
 
-// Workgroup g of group a (shard table sht) -- the whole kernel body.
+// Workgroup g of group a (shard table sht) -- the whole kernel body.  The range, cursor,
+// occurrence, LDS and global index arithmetic is gemv1_plan.h's (shared with the CPU address
+// replay).
 template <int K, int CB, bool ONE, int R>
 __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, const int g, uint32_t* lds)
 {
-    // shard table entry; a single-shard group (ONE) only ever reads entry 0
-    auto sh = [&](int s) -> const G1Shard& { return sht[ONE ? 0 : s]; };
+    auto sh = [&](int s) -> const G1Shard& { return g1_sh<ONE>(sht, s); };
     constexpr int D = g1_depth(K);
 
-    const int ntr = a.ntr;
-    const int ub = g1_first_unit(a, g), L = a.q + (g < a.r ? 1 : 0);
+    const G1Range w = g1_range<ONE>(a, sht, g);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     __builtin_amdgcn_s_setprio(3);
 
-    // ---- this wave's units: the contiguous run ub + lo .. ub + lo + n - 1 of the range
-    const int lo = (wave * L) >> 3;
-    const int n = (((wave + 1) * L) >> 3) - lo;
-    const uint32_t lk = lane * K;
+    // ---- this wave's units: the contiguous run w.ub + lo .. w.ub + lo + n - 1 of the range
+    const G1Run run = g1_wave_run(w.L, wave);
+    const int n = run.n;
+    const uint32_t lk = g1_lane_word(lane, K);
     const bool first_lane = (lane & 7) == 0;
-
-    // Wave-uniform cursor over the wave's units: shard, column group, tile row, segment and
-    // the first word of the unit's 8 tiles.  Consecutive units are consecutive tile rows
-    // (ntr >= 8); only a column-group crossing reads the shard table again.
-    struct Cursor {
-        int s, cg, tr, S;
-        long stride;   // words between consecutive tile rows
-        const uint32_t* p;
-    };
-    auto seat = [&](Cursor& q) {
-        q.stride = (long)sh(q.s).oc16 * (8 * K);
-        q.p = sh(q.s).trellis + ((long)q.tr * sh(q.s).oc16 + 8 * q.cg) * (8 * K);
-    };
-    auto cursor_at = [&](int u) {
-        Cursor q;
-        q.s = g1_shard_of_unit<ONE>(a, sht, u);
-        const int rel = u - sh(q.s).ubeg;
-        q.cg = g1_div(rel, a.dntr);
-        q.tr = rel - q.cg * ntr;
-        q.S = sh(q.s).sbeg + q.cg;
-        seat(q);
-        return q;
-    };
-    auto advance = [&](Cursor& q) {
-        q.tr++;
-        q.p += q.stride;
-        if (q.tr == ntr) {
-            q.tr = 0;
-            q.S++;
-            if (++q.cg == sh(q.s).ncg) {
-                q.s++;
-                q.cg = 0;
-            }
-            seat(q);
-        }
-    };
 
     // A unit's loads: the lane's K words.  Prefetch cursor (D units ahead; it stops at the
     // wave's last unit, whose data is then loaded again and not used) and processing cursor.
@@ -284,77 +143,41 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     struct Slot {
         uint32_t w[K + 1];
     };
-    auto load = [&](Slot& sl, const Cursor& q) { g1_load<K>(sl.w, q.p, lk); };
-    Cursor pf = cursor_at(ub + lo), cu = pf;
+    auto load = [&](Slot& sl, const G1Cursor& q) { g1_load<K>(sl.w, q.p, lk); };
+    G1Cursor pf = g1_cursor_at<K, ONE>(a, sht, w.ub + run.lo), cu = pf;
     int jpf = 0;
-    auto next_pf = [&]() -> const Cursor& {
-        if (jpf + 1 < n) {
-            jpf++;
-            advance(pf);
-        }
+    auto next_pf = [&]() -> const G1Cursor& {
+        g1_next_pf<K, ONE>(a, sht, pf, jpf, n);
         return pf;
     };
     Slot ring[D];
 
-    // ---- this workgroup's segments: S_first .. S_first + nseg - 1
-    const int s_first = g1_shard_of_unit<ONE>(a, sht, ub);
-    const int S_first = sh(s_first).sbeg + g1_div(ub - sh(s_first).ubeg, a.dntr);
-    const int nseg = [&] {
-        const int u = ub + L - 1;
-        const int s = g1_shard_of_unit<ONE>(a, sht, u);
-        return sh(s).sbeg + g1_div(u - sh(s).ubeg, a.dntr) - S_first + 1;
-    }();
-    // The range's 128-input blocks in the order its units meet them ("occurrences"): the
-    // first segment's tile rows tr0 .. tre0 (blocks tr0 / 8 .. tre0 / 8), then every later
-    // segment from tile row 0 on (ntr / 8 blocks each, the last one possibly fewer).
-    // Occurrence of unit (segment S_first + k, tile row tr): see occ_of.
-    const int tr0 = ub - sh(s_first).ubeg - (S_first - sh(s_first).sbeg) * ntr;
-    const int nbpc = ntr >> 3;
-    const int nb0 = (min(ntr - 1, tr0 + L - 1) >> 3) - (tr0 >> 3) + 1;
-    auto occ_of = [&](int k, int tr) { return k == 0 ? (tr >> 3) - (tr0 >> 3) : nb0 + (k - 1) * nbpc + (tr >> 3); };
-    const int nocc = [&] {
-        const int u = ub + L - 1;
-        const int s = g1_shard_of_unit<ONE>(a, sht, u);
-        const int rel = u - sh(s).ubeg;
-        const int cg = g1_div(rel, a.dntr);
-        return occ_of(sh(s).sbeg + cg - S_first, rel - cg * ntr) + 1;
-    }();
-
-    // LDS: red[nseg][G1_NW][R][128] fp32 partial rows | act[nocc][8][R][16] duplicated fp16
-    // activations | zero[16] (the A operand of the lanes whose k-block is not theirs)
+    const G1Lds ll = g1_lds_layout(w.nseg, w.nocc, R);
     float* red = reinterpret_cast<float*>(lds);
-    uint32_t* act = reinterpret_cast<uint32_t*>(red + nseg * G1_NW * R * 128);
-    uint32_t* zero = act + nocc * R * 128;
+    uint32_t* act = lds + ll.act;
+    uint32_t* zero = lds + ll.zero;
     if (threadIdx.x < 16) zero[threadIdx.x] = 0u;
-    for (int k = 0; k < nseg; k++)
+    for (int k = 0; k < w.nseg; k++)
 #pragma unroll
         for (int r = 0; r < R; r++)
-            *reinterpret_cast<float2*>(red + ((k * G1_NW + wave) * R + r) * 128 + 2 * lane) = float2{0.f, 0.f};
+            *reinterpret_cast<float2*>(red + g1_red_row(k, wave, R, r) + 2 * lane) = float2{0.f, 0.f};
     const Dot2Consts kc = dot2_consts();
-    const long ic = (long)ntr * 16;
 
-    // Activations, once per workgroup: the waves share out the occurrences; each transforms its block of every activation row r,
-    // fp16(H128(x_r * suh)) (lane l: outputs 2l, 2l + 1 = rows 2(l % 8), 2(l % 8) + 1 of the
-    // block's tile row l / 8) and stores each output as a duplicated fp16 pair in the order
-    // the MFMAs read them: act[occurrence][tile row][r][m][t] holds row 2m + {0, 1, 8, 9}[t]
-    // (so lane l's two rows go to m = l % 4, t = 2 ((l % 8) / 4) and t + 1).  Rows
-    // r >= nrows repeat the last row (their results are not stored).
-    for (int i = wave; i < nocc; i += G1_NW) {
-        int k = 0, blk = (tr0 >> 3) + i;
-        if (i >= nb0) {
-            const int j = i - nb0;
-            k = 1 + g1_div(8 * j, a.dntr);          // j / nbpc
-            blk = j - (k - 1) * nbpc;
-        }
-        const int s = g1_shard_of_seg<ONE>(a, sht, S_first + k);
+    // Activations, once per workgroup: the waves share out the occurrences; each transforms
+    // its block of every activation row r, fp16(H128(x_r * suh)) (lane l: outputs 2l, 2l + 1
+    // = rows 2(l % 8), 2(l % 8) + 1 of the block's tile row l / 8) and stores each output as a
+    // duplicated fp16 pair in the order the MFMAs read them (g1_act_word).
+    for (int i = wave; i < w.nocc; i += G1_NW) {
+        int k, blk;
+        g1_occ_block(a, w, i, k, blk);
+        const int s = g1_shard_of_seg<ONE>(a, sht, w.S_first + k);
         const uint32_t sw = reinterpret_cast<const uint32_t*>(sh(s).suh + blk * 128)[lane];
 #pragma unroll 1
         for (int r = 0; r < R; r++) {
-            const uint32_t xw = reinterpret_cast<const uint32_t*>(a.x + min(r, a.nrows - 1) * ic + blk * 128)[lane];
+            const uint32_t xw = reinterpret_cast<const uint32_t*>(a.x + g1_x_elem(a, r, blk))[lane];
             float v0 = g1_lo(xw) * g1_lo(sw), v1 = g1_hi(xw) * g1_hi(sw);
             wave_fwht128(v0, v1);
-            *reinterpret_cast<uint2*>(act + ((i * 8 + (lane >> 3)) * R + r) * 16 + 4 * (lane & 3) + 2 * ((lane >> 2) & 1)) =
-                uint2{g1_dup(v0), g1_dup(v1)};
+            *reinterpret_cast<uint2*>(act + g1_act_word(i, lane, R, r)) = uint2{g1_dup(v0), g1_dup(v1)};
         }
     }
     // The first unit's loads go out after the wave's activation loads have returned, so those
@@ -376,20 +199,15 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     // yacc[h][e] of lane 16r + n: activation row r's sum for output 32e + 16(n / 8) + n % 8 + 8h
     // (lanes 16r + n with r >= R hold copies of row R - 1).
     f32x4 yacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-    const int yrow = lane >> 4, ycol = 16 * ((lane >> 3) & 1) + (lane & 7);
-    // This lane's A operand: row i = lane % 16 in k-block lane / 16, which carries activation
-    // row i / 4 when i % 4 is that k-block and zeros otherwise.  Its LDS byte address for a
-    // unit whose table entry starts at byte e: e * asel + aoff.
-    const uint32_t asel = ((lane & 15) & 3) == (lane >> 4) ? 1u : 0u;
-    const uint32_t aoff = asel ? (uint32_t)((reinterpret_cast<char*>(act) - reinterpret_cast<char*>(lds)) +
-                                            min((lane & 15) >> 2, R - 1) * 64)
-                               : (uint32_t)(reinterpret_cast<char*>(zero) - reinterpret_cast<char*>(lds));
-    int cur = cu.S - S_first;
-    int occ = occ_of(cur, cu.tr);
+    const int yrow = g1_yrow(lane), ycol = g1_ycol(lane);
+    const uint32_t asel = g1_asel(lane);
+    const uint32_t aoff = g1_aoff(lane, R, ll);
+    int cur = cu.S - w.S_first;
+    int occ = g1_occ_of(w, cur, cu.tr);
     const int pq1 = (n + 3) >> 2, pq2 = (n + 1) >> 1, pq3 = (3 * n + 3) >> 2;
     auto flush = [&](int k) {
         if (yrow < R) {
-            float* rr = red + ((cur * G1_NW + wave) * R + yrow) * 128 + ycol;
+            float* rr = red + g1_red_row(cur, wave, R, yrow) + ycol;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 rr[32 * e] = yacc[0][e];
@@ -403,14 +221,14 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
 #pragma unroll
         for (int d = 0; d < D; d++) {
             if (d == 0 || j + d < n) {
-                if (cu.S - S_first != cur) flush(cu.S - S_first);
-                const uint32_t e = (uint32_t)((occ * 8 + (cu.tr & 7)) * R) * 64u;
+                if (cu.S - w.S_first != cur) flush(cu.S - w.S_first);
+                const uint32_t e = g1_a_entry(occ, cu.tr, R);
                 const f16x8* ap = reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(lds) + (__umul24(e, asel) + aoff));
                 const f16x8 av[4] = {ap[0], ap[1], ap[2], ap[3]};
                 chunk_prev_dpp<K>(ring[d].w, first_lane);
                 g1_mfma_chunk<K, CB>(ring[d].w, av, yacc, kc);
                 if (j + d + 1 < n) {
-                    advance(cu);
+                    g1_advance<K, ONE>(a, sht, cu);
                     occ += (cu.tr & 7) == 0;
                 }
                 // priority 3, 2, 1, 0 over the run's four quarters
@@ -428,7 +246,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
 
     // ---- per segment: fixed-order sum of the waves; finish here, or via the slots
     auto finish = [&](int k, int r, float v0, float v1) {
-        const int S = S_first + k;
+        const int S = w.S_first + k;
         const int s = g1_shard_of_seg<ONE>(a, sht, S);
         const int cg = S - sh(s).sbeg;
         wave_fwht128(v0, v1);
@@ -439,35 +257,28 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
                              ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
         reinterpret_cast<uint32_t*>(sh(s).C + r * sh(s).ldc + cg * 128)[lane] = out;
     };
-    auto contributors = [&](int k, int& g_lo, int& g_hi) {
-        const int S = S_first + k;
-        const int s = g1_shard_of_seg<ONE>(a, sht, S);
-        const int segU0 = sh(s).ubeg + (S - sh(s).sbeg) * ntr;
-        g_lo = g1_wg_of(a, segU0);
-        g_hi = g1_wg_of(a, segU0 + ntr - 1);
-    };
     const int nr = R == 1 ? 1 : a.nrows;
-    for (int k = wave; k < nseg; k += G1_NW) {
+    for (int k = wave; k < w.nseg; k += G1_NW) {
         float v0[R], v1[R];
 #pragma unroll
         for (int r = 0; r < R; r++) {
             v0[r] = v1[r] = 0.f;
 #pragma unroll
             for (int ww = 0; ww < G1_NW; ww++) {
-                const float2 p = *reinterpret_cast<const float2*>(red + ((k * G1_NW + ww) * R + r) * 128 + 2 * lane);
+                const float2 p = *reinterpret_cast<const float2*>(red + g1_red_row(k, ww, R, r) + 2 * lane);
                 v0[r] += p.x;
                 v1[r] += p.y;
             }
         }
         int g_lo, g_hi;
-        contributors(k, g_lo, g_hi);
+        g1_contributors<ONE>(a, sht, w.S_first + k, g_lo, g_hi);
         if (g_hi > g_lo) {
-            // split segment: slot (S + g) holds this workgroup's R rows of 128 partials, which
+            // split segment: slot (S, g) holds this workgroup's R rows of 128 partials, which
             // gemv1_finish_kernel adds after the launch
-            uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + (long)(S_first + k + g) * R * 128) + lane;
+            uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + g1_slot(w.S_first + k, g, R)) + lane;
 #pragma unroll
             for (int r = 0; r < R; r++)
-                my[r * 64] = (uint64_t)__builtin_bit_cast(uint32_t, v0[r]) |
+                my[g1_slot_word(0, R, r)] = (uint64_t)__builtin_bit_cast(uint32_t, v0[r]) |
                              ((uint64_t)__builtin_bit_cast(uint32_t, v1[r]) << 32);
         } else {
             for (int r = 0; r < nr; r++) finish(k, r, v0[r], v1[r]);
@@ -494,11 +305,7 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     // by-value parameter with a run-time group would make the compiler copy all of it to
     // scratch memory first.
     const G1Multi& mm = *(const G1Multi*)__builtin_amdgcn_kernarg_segment_ptr();
-    int i = 0;
-#pragma unroll
-    for (int j = 1; j < G1_MAXSH; j++)
-        if (j < mm.ngrp && (int)blockIdx.x >= mm.gbeg[j]) i = j;
-    i = __builtin_amdgcn_readfirstlane(i);
+    const int i = __builtin_amdgcn_readfirstlane(g1_group_of(mm.gbeg, mm.ngrp, (int)blockIdx.x));
     const G1Group& a = mm.grp[i];
     const G1Shard* sht = mm.sh + mm.sh0[i];
     const int g = blockIdx.x - mm.gbeg[i];
@@ -525,25 +332,25 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
 template <int R, bool ONE>
 __device__ __forceinline__ void g1_finish_body(const G1Group& a, const G1Shard* sht, int S)
 {
-    auto sh = [&](int s) -> const G1Shard& { return sht[ONE ? 0 : s]; };
+    auto sh = [&](int s) -> const G1Shard& { return g1_sh<ONE>(sht, s); };
     if (S >= a.nsegs) return;
     const int s = g1_shard_of_seg<ONE>(a, sht, S);
     const int cg = S - sh(s).sbeg;
-    const int segU0 = sh(s).ubeg + cg * a.ntr;
-    const int g_lo = g1_wg_of(a, segU0), g_hi = g1_wg_of(a, segU0 + a.ntr - 1);
+    int g_lo, g_hi;
+    g1_contributors<ONE>(a, sht, S, g_lo, g_hi);
     if (g_hi == g_lo) return;
     const int lane = threadIdx.x;
     const int nsl = g_hi - g_lo + 1;
     const int nr = R == 1 ? 1 : a.nrows;
     const uint32_t sv = reinterpret_cast<const uint32_t*>(sh(s).svh + cg * 128)[lane];
-    const uint64_t* sl = reinterpret_cast<const uint64_t*>(a.slots + (long)(S + g_lo) * R * 128) + lane;
+    const uint64_t* sl = reinterpret_cast<const uint64_t*>(a.slots + g1_slot(S, g_lo, R)) + lane;
     constexpr int B = 32;
     for (int r = 0; r < nr; r++) {
         float v0 = 0.f, v1 = 0.f;
         for (int t0 = 0; t0 < nsl; t0 += B) {
             uint64_t xv[B];
 #pragma unroll
-            for (int t = 0; t < B; t++) xv[t] = sl[((long)min(t0 + t, nsl - 1) * R + r) * 64];
+            for (int t = 0; t < B; t++) xv[t] = sl[g1_slot_word(min(t0 + t, nsl - 1), R, r)];
 #pragma unroll
             for (int t = 0; t < B; t++)
                 if (t0 + t < nsl) {
@@ -572,11 +379,7 @@ template <int R>
 __global__ __launch_bounds__(64) void gemv1_finish_multi_kernel(const G1Multi)
 {
     const G1Multi& mm = *(const G1Multi*)__builtin_amdgcn_kernarg_segment_ptr();
-    int i = 0;
-#pragma unroll
-    for (int j = 1; j < G1_MAXSH; j++)
-        if (j < mm.ngrp && (int)blockIdx.x >= mm.fbeg[j]) i = j;
-    i = __builtin_amdgcn_readfirstlane(i);
+    const int i = __builtin_amdgcn_readfirstlane(g1_group_of(mm.fbeg, mm.ngrp, (int)blockIdx.x));
     g1_finish_body<R, false>(mm.grp[i], mm.sh + mm.sh0[i], blockIdx.x - mm.fbeg[i]);
 }
 
@@ -616,138 +419,10 @@ static int g1_cu_count()
     return cus;
 }
 
-static G1Div g1_magic(uint32_t d)
-{
-    int l = 0;
-    while ((1ull << l) < d) l++;
-    return G1Div{(uint32_t)(((1ull << (31 + l)) / d) + 1), l - 1};
-}
-
-// Dynamic LDS a launch needs: a partial row per wave for the most segments (shard, column
-// group) a workgroup range of ceil(U / G) units can touch, a transformed activation block for
-// each 128-input block it can meet (at most ceil(L / 8) + nseg + 1: a piece of a segment
-// meets one block more than its length in blocks when it starts inside a block, and only the
-// first piece can), and the 64-byte zero operand.
-static size_t g1_lds_bytes(int U, int G, int ntr, int R)
-{
-    const int L = (U + G - 1) / G;
-    const int nseg = (L - 1 + ntr - 1) / ntr + 1;
-    const int nocc = (L + 7) / 8 + nseg + 1;
-    return (size_t)nseg * G1_NW * R * 128 * sizeof(float) + (size_t)nocc * R * 128 * sizeof(uint32_t) + 64;
-}
-
-// Row-count template of a call: one activation row, or up to four (G1_ROWS).
-constexpr int G1_ROWS = 4;
-static int g1_R(int rows) { return rows == 1 ? 1 : G1_ROWS; }
-
-// Per-shard share of the workspace after the counter area: slots of R rows for up to
-// G1_GMAX workgroups and one per column group.
 size_t gemv1_slot_bytes(int ic, int oc, int rows)
 {
     (void)ic;
-    return (size_t)(G1_GMAX + oc / 128) * g1_R(rows) * 128 * sizeof(float);
-}
-
-// Units per workgroup the launch aims for: fewer, longer ranges cut the cross-workgroup
-// reduction (fewer contributors per column group) and the per-wave start-up, while a
-// launch still spreads over up to G1_WG_PER_CU workgroups per CU.  Measured on MI355X
-// over the 27B projection shapes: 32 is best or within 3% of best for each.
-constexpr int G1_UNITS_PER_WG = 32;
-
-// Fills one group from shards[idx[0..n-1]] (same K and codebook) into table entries
-// tab[0..n-1]; returns its unit count.
-static long g1_group(G1Group& grp, G1Shard* tab, const GemvShard* shards, const int* idx, int n, const uint16_t* A,
-                     int ntr, int rows)
-{
-    grp = G1Group{};
-    grp.x = A;
-    grp.nrows = rows;
-    grp.ntr = ntr;
-    grp.nshards = n;
-    long U = 0;
-    int nsegs = 0;
-    for (int j = 0; j < n; j++) {
-        const GemvShard& d = shards[idx[j]];
-        G1Shard& e = tab[j];
-        e.trellis = d.trellis;
-        e.suh = d.suh;
-        e.svh = d.svh;
-        e.C = d.C;
-        e.ldc = d.ldc;
-        e.ubeg = (int)U;
-        e.sbeg = nsegs;
-        e.oc16 = d.oc / 16;
-        e.ncg = d.oc / 128;
-        U += (long)(d.oc / 128) * ntr;
-        nsegs += d.oc / 128;
-    }
-    grp.nsegs = nsegs;
-    return U;
-}
-
-// Workgroup split of a group of U units into G ranges, and its share of the slots.
-static int g1_place(G1Group& grp, long U, int G, int R, char* slots, size_t& sbase, size_t slot_bytes)
-{
-    if (U > (1L << 30))
-        return set_error(EXL3_ERR_ARG, "exl3_gemv: %ld tile-row units in one launch (limit 2^30)", U);
-    const size_t need = (size_t)(G + grp.nsegs) * R * 128 * sizeof(float);
-    if (sbase + need > slot_bytes)
-        return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: slot area of %zu bytes, %zu needed", slot_bytes,
-                         sbase + need);
-    grp.U = (int)U;
-    grp.G = G;
-    grp.q = (int)(U / G);
-    grp.r = (int)(U % G);
-    // divisors are >= 8 (ntr = ic / 16 with ic >= 128; G <= U / 8), as g1_div requires
-    grp.dntr = g1_magic((uint32_t)grp.ntr);
-    grp.dq = g1_magic((uint32_t)grp.q);
-    grp.dq1 = g1_magic((uint32_t)grp.q + 1);
-    grp.slots = reinterpret_cast<float*>(slots + sbase);
-    sbase += need;
-    return EXL3_OK;
-}
-
-// Whether some segment of the group lies in more than one workgroup range (then the
-// launch needs gemv1_finish_kernel): segment S is units S ntr .. S ntr + ntr - 1.
-static bool g1_any_split(const G1Group& grp)
-{
-    const long big = (long)grp.r * (grp.q + 1);
-    auto wg_of = [&](long u) { return u < big ? u / (grp.q + 1) : grp.r + (u - big) / grp.q; };
-    for (int S = 0; S < grp.nsegs; S++)
-        if (wg_of((long)S * grp.ntr) != wg_of((long)S * grp.ntr + grp.ntr - 1)) return true;
-    return false;
-}
-
-// The finish kernel of a single-group launch, if any of its segments is split.
-static int g1_finish(G1Args& args, int R, bool one, hipStream_t stream)
-{
-    if (!g1_any_split(args.grp)) return EXL3_OK;
-    const void* fn = R == 1 ? (one ? reinterpret_cast<const void*>(&gemv1_finish_kernel<1, true>)
-                                   : reinterpret_cast<const void*>(&gemv1_finish_kernel<1, false>))
-                            : (one ? reinterpret_cast<const void*>(&gemv1_finish_kernel<G1_ROWS, true>)
-                                   : reinterpret_cast<const void*>(&gemv1_finish_kernel<G1_ROWS, false>));
-    void* kargs[] = {&args};
-    hipLaunchKernel(fn, dim3(args.grp.nsegs), dim3(64), kargs, 0, stream);
-    return check_launch("exl3_gemv (1-4 rows, split segments)");
-}
-
-// The finish kernel of a multi-group launch (m.grp[0 .. m.ngrp - 1], m.sh, m.sh0 set), if any
-// of its segments is split.
-static int g1_finish(G1Multi& m, int R, hipStream_t stream)
-{
-    bool any = false;
-    int nb = 0;
-    for (int t = 0; t < m.ngrp; t++) {
-        m.fbeg[t] = nb;
-        nb += m.grp[t].nsegs;
-        any = any || g1_any_split(m.grp[t]);
-    }
-    if (!any) return EXL3_OK;
-    const void* fn = R == 1 ? reinterpret_cast<const void*>(&gemv1_finish_multi_kernel<1>)
-                            : reinterpret_cast<const void*>(&gemv1_finish_multi_kernel<G1_ROWS>);
-    void* kargs[] = {&m};
-    hipLaunchKernel(fn, dim3(nb), dim3(64), kargs, 0, stream);
-    return check_launch("exl3_gemv (1-4 rows, split segments)");
+    return g1_slot_bytes(oc, rows);
 }
 
 static int g1_launch(const void* fn, void* arg, int G, size_t lds, hipStream_t stream)
@@ -759,29 +434,6 @@ static int g1_launch(const void* fn, void* arg, int G, size_t lds, hipStream_t s
     void* kargs[] = {arg};
     hipLaunchKernel(fn, dim3(G), dim3(64 * G1_NW), kargs, lds, stream);
     return check_launch("exl3_gemv (1-4 rows)");
-}
-
-// Workgroup counts G[0..ns) of one launch whose groups have U[t] units, for the most
-// workgroups per CU (up to G1_WG_PER_CU) whose LDS lets them all stay resident; returns
-// that number and the launch's LDS per workgroup.
-static int g1_split(const long* U, int ns, int ntr, int R, int cus, int* G, size_t& lds)
-{
-    constexpr size_t LDS_PER_CU = 160 * 1024;
-    int wgpc = G1_WG_PER_CU;
-    for (; wgpc >= 1; wgpc--) {
-        const int gmax = std::min(G1_GMAX, wgpc * cus);
-        long Gsum = 0;
-        for (int t = 0; t < ns; t++) {
-            G[t] = (int)std::min<long>(gmax, std::max<long>(1, U[t] / G1_UNITS_PER_WG));
-            Gsum += G[t];
-        }
-        if (Gsum > gmax)   // share the resident workgroups in proportion to the groups' sizes
-            for (int t = 0; t < ns; t++) G[t] = std::max(1, (int)((long)G[t] * gmax / Gsum));
-        lds = 0;
-        for (int t = 0; t < ns; t++) lds = std::max(lds, g1_lds_bytes((int)U[t], G[t], ntr, R));
-        if ((size_t)wgpc * lds <= LDS_PER_CU) break;
-    }
-    return std::max(wgpc, 1);
 }
 
 // Whether 2..4 rows of these shards run well here: every launch keeps at least three
@@ -808,94 +460,39 @@ bool gemv1_rows_fit(const GemvShard* shards, int nshards)
     return true;
 }
 
-// 1..4 activation rows: the shards are grouped by (K, codebook), at most G1_MAXSH shards a
-// group.  A launch takes whole groups of one codebook, at most G1_MAXSH shards in all: one
-// group is a gemv1_kernel launch, several share a gemv1_multi_kernel launch with their
-// workgroup counts scaled to the resident limit together.  Workgroups per CU: four, or
-// fewer where a launch's LDS per workgroup (larger with four rows) would not let four
-// stay resident.
+// The launches of g1_plan: the decode kernel, then (if some segment is split) the finish
+// kernel, one block per segment.
 int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
                    size_t slot_bytes, hipStream_t stream)
 {
-    if (rows < 1 || rows > G1_ROWS) return set_error(EXL3_ERR_ARG, "exl3_gemv: rows=%d is not in 1..%d", rows, G1_ROWS);
-    const int R = g1_R(rows);
-    const int ic = shards[0].ic;
-    const int ntr = ic / 16;
-    const int cus = g1_cu_count();
-
-    // groups: shard indices by (codebook, K) in first-seen order, split every G1_MAXSH shards
-    constexpr int MAXG = EXL3_MAX_SHARDS;
-    int gidx[MAXG][G1_MAXSH], gn[MAXG] = {0}, gK[MAXG], gcb[MAXG], ng = 0;
-    for (int i = 0; i < nshards; i++) {
-        if (shards[i].K < 1 || shards[i].K > 8)
-            return set_error(EXL3_ERR_ARG, "exl3_gemv: K=%d is not in 1..8", shards[i].K);
-        int j = ng - 1;
-        while (j >= 0 && !(gK[j] == shards[i].K && gcb[j] == shards[i].cb && gn[j] < G1_MAXSH)) j--;
-        if (j < 0) {
-            j = ng++;
-            gK[j] = shards[i].K;
-            gcb[j] = shards[i].cb;
+    return g1_plan(A, shards, nshards, rows, slots, slot_bytes, g1_cu_count(), [&](const G1Launch& L) {
+        const char* what = "exl3_gemv (1-4 rows, split segments)";
+        if (!L.multi) {
+            G1Args args = *L.args;
+            const void* fn = L.R == 1 ? g1_fn_kcb<1>(L.K, L.cb, L.one) : g1_fn_kcb<G1_ROWS>(L.K, L.cb, L.one);
+            int rc = g1_launch(fn, &args, L.G, L.lds, stream);
+            if (rc != EXL3_OK || !L.finish) return rc;
+            const void* ff = L.R == 1 ? (L.one ? reinterpret_cast<const void*>(&gemv1_finish_kernel<1, true>)
+                                               : reinterpret_cast<const void*>(&gemv1_finish_kernel<1, false>))
+                                      : (L.one ? reinterpret_cast<const void*>(&gemv1_finish_kernel<G1_ROWS, true>)
+                                               : reinterpret_cast<const void*>(&gemv1_finish_kernel<G1_ROWS, false>));
+            void* kargs[] = {&args};
+            hipLaunchKernel(ff, dim3(L.fblocks), dim3(64), kargs, 0, stream);
+            return check_launch(what);
         }
-        gidx[j][gn[j]++] = i;
-    }
-
-    size_t sbase = 0;
-    bool done[MAXG] = {false};
-    for (int j0 = 0; j0 < ng; j0++) {
-        if (done[j0]) continue;
-        // this launch: group j0 and the following groups of its codebook while they fit
-        int sel[G1_MAXSH], ns = 0, nsh = 0;
-        for (int j = j0; j < ng; j++)
-            if (!done[j] && gcb[j] == gcb[j0] && nsh + gn[j] <= G1_MAXSH) {
-                sel[ns++] = j;
-                nsh += gn[j];
-                done[j] = true;
-            }
-        const int cb = gcb[j0];
-        G1Multi m = {};
-        long U[G1_MAXSH];
-        int G[G1_MAXSH], sh0 = 0;
-        for (int t = 0; t < ns; t++) {
-            const int j = sel[t];
-            m.sh0[t] = sh0;
-            m.K[t] = gK[j];
-            U[t] = g1_group(m.grp[t], m.sh + sh0, shards, gidx[j], gn[j], A, ntr, rows);
-            sh0 += gn[j];
-        }
-        size_t lds = 0;
-        g1_split(U, ns, ntr, R, cus, G, lds);
-        if (ns == 1) {
-            G1Args args = {};
-            args.grp = m.grp[0];
-            for (int i = 0; i < gn[sel[0]]; i++) args.sh[i] = m.sh[i];
-            int rc = g1_place(args.grp, U[0], G[0], R, slots, sbase, slot_bytes);
-            if (rc != EXL3_OK) return rc;
-            const bool one = gn[sel[0]] == 1;
-            const void* fn = R == 1 ? g1_fn_kcb<1>(gK[sel[0]], cb, one) : g1_fn_kcb<G1_ROWS>(gK[sel[0]], cb, one);
-            rc = g1_launch(fn, &args, G[0], lds, stream);
-            if (rc != EXL3_OK) return rc;
-            rc = g1_finish(args, R, one, stream);
-            if (rc != EXL3_OK) return rc;
-            continue;
-        }
-        int gb = 0;
-        for (int t = 0; t < ns; t++) {
-            const int rc = g1_place(m.grp[t], U[t], G[t], R, slots, sbase, slot_bytes);
-            if (rc != EXL3_OK) return rc;
-            m.gbeg[t] = gb;
-            gb += G[t];
-        }
-        m.ngrp = ns;
-        const void* fn = R == 1 ? (cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG, 1>)
-                                               : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST, 1>))
-                                : (cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG, G1_ROWS>)
-                                               : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST, G1_ROWS>));
-        int rc = g1_launch(fn, &m, gb, lds, stream);
-        if (rc != EXL3_OK) return rc;
-        rc = g1_finish(m, R, stream);
-        if (rc != EXL3_OK) return rc;
-    }
-    return EXL3_OK;
+        G1Multi m = *L.m;
+        const void* fn = L.R == 1 ? (L.cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG, 1>)
+                                                    : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST, 1>))
+                                  : (L.cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG, G1_ROWS>)
+                                                    : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST, G1_ROWS>));
+        int rc = g1_launch(fn, &m, L.G, L.lds, stream);
+        if (rc != EXL3_OK || !L.finish) return rc;
+        const void* ff = L.R == 1 ? reinterpret_cast<const void*>(&gemv1_finish_multi_kernel<1>)
+                                  : reinterpret_cast<const void*>(&gemv1_finish_multi_kernel<G1_ROWS>);
+        void* kargs[] = {&m};
+        hipLaunchKernel(ff, dim3(L.fblocks), dim3(64), kargs, 0, stream);
+        return check_launch(what);
+    });
 }
 
 }  // namespace exl3

@@ -1,0 +1,870 @@
+// CPU address replay of the GEMV and stream-K GEMM kernels (test tool, not part of the C ABI).
+//
+// A call plans a launch sequence with the product's own planning code (g1_plan of
+// gemv1_plan.h, sk_plan_* of gemm_sk_plan.h) over fake device buffers, then walks every
+// workgroup, wave and lane of each launch through the same __host__ __device__ index
+// functions the kernels call, in the kernels' loop order, and checks
+//   * every global load and store against the buffer it addresses (trellis, suh, svh,
+//     activations, outputs, slots, counters), every LDS access against the launch's
+//     dynamic LDS and the region it belongs to;
+//   * coverage: each unit / K-step decoded exactly once, each output element written exactly
+//     once, each slot read after the launch that writes it and holding the partial the
+//     reader expects (segment or tile, workgroup, row), each activation-table read of the
+//     occurrence and block the unit needs.
+// Nothing here runs on a GPU; the library is built with hipcc only because the shared index
+// functions are marked __host__ __device__.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../gemm_sk_plan.h"
+#include "../gemv1_plan.h"
+
+namespace exl3 {
+
+// The product's error recorder, as the planning code calls it.
+thread_local char g_err[512];
+
+int set_error(int code, const char* fmt, ...)
+{
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int check_launch(const char*) { return EXL3_OK; }
+
+}  // namespace exl3
+
+using namespace exl3;
+
+namespace {
+
+thread_local std::string g_msg;
+
+// Fake device buffers: buffer b starts at b << 40, so any address maps back to (buffer,
+// byte offset) and an index outside a buffer cannot land in another one.
+constexpr int FAKE_SHIFT = 40;
+enum Buf { B_NONE, B_X, B_C, B_SLOTS, B_WS, B_TRELLIS = 16, B_SUH = 48, B_SVH = 80, B_AH = 112 };
+
+inline uintptr_t fake(int b) { return (uintptr_t)b << FAKE_SHIFT; }
+template <class T>
+inline T* fake_ptr(int b) { return reinterpret_cast<T*>(fake(b)); }
+inline int buf_of(const void* p) { return (int)((uintptr_t)p >> FAKE_SHIFT); }
+inline long off_of(const void* p) { return (long)((uintptr_t)p & (((uintptr_t)1 << FAKE_SHIFT) - 1)); }
+
+struct Fail {
+    std::string what;
+};
+
+[[noreturn]] void fail(const char* fmt, ...)
+{
+    char b[640];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(b, sizeof b, fmt, ap);
+    va_end(ap);
+    throw Fail{b};
+}
+
+// A byte range [p, p + n) must lie inside buffer `buf` of `size` bytes.
+void need_in(const void* p, long n, int buf, long size, const char* what)
+{
+    if (buf_of(p) != buf) fail("%s: address in buffer %d, expected buffer %d", what, buf_of(p), buf);
+    const long o = off_of(p);
+    if (o < 0 || o + n > size) fail("%s: bytes [%ld, %ld) outside [0, %ld)", what, o, o + n, size);
+}
+
+struct ShardSpec {
+    int ic, oc, K, cb;
+};
+
+// ================================================================ gemv1
+
+struct G1World {
+    int rows, ic;
+    std::vector<ShardSpec> sh;
+    std::vector<int> col0;        // first output column of each shard in C
+    long ldc;
+    size_t slot_bytes;
+    std::vector<uint8_t> out;     // writes per (row, column)
+    long units_total = 0;
+    std::vector<uint8_t> unit_seen;          // per shard-local unit id, offset by shard
+    std::vector<long> unit_base;
+    // slots: float offset of each row start -> (S, g, r) that wrote it
+    std::map<long, std::tuple<int, int, int>> slot_rows;
+    long loads = 0, lds_reads = 0;
+};
+
+int shard_index(const G1World& w, const GemvShard* shards, const uint32_t* trellis)
+{
+    for (size_t i = 0; i < w.sh.size(); i++)
+        if (shards[i].trellis == trellis) return (int)i;
+    return -1;
+}
+
+template <int K, bool ONE, int R>
+void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G1Shard* sht, int g, size_t lds,
+                  int launch)
+{
+    const G1Range w = g1_range<ONE>(a, sht, g);
+    if (w.L < 1) fail("launch %d wg %d: empty range", launch, g);
+    if (w.nseg < 1 || w.nocc < 1) fail("launch %d wg %d: nseg %d nocc %d", launch, g, w.nseg, w.nocc);
+    const G1Lds ll = g1_lds_layout(w.nseg, w.nocc, R);
+    if ((size_t)ll.words * 4 > lds)
+        fail("launch %d wg %d: LDS layout %d bytes > launch LDS %zu", launch, g, ll.words * 4, lds);
+    const int ntr = a.ntr;
+    const long ic = (long)ntr * 16;
+
+    auto shard_of = [&](int s) -> int {
+        if (s < 0 || s >= a.nshards) fail("launch %d wg %d: shard %d of %d", launch, g, s, a.nshards);
+        return shard_index(W, shards, g1_sh<ONE>(sht, s).trellis);
+    };
+    auto trellis_words = [&](int gi) { return (long)(W.sh[gi].ic / 16) * (W.sh[gi].oc / 16) * 8 * K; };
+
+    // ---- zero operand and partial rows
+    for (int t = 0; t < 16; t++)
+        if (ll.zero + t >= ll.words) fail("zero word out of LDS");
+    for (int k = 0; k < w.nseg; k++)
+        for (int wave = 0; wave < G1_NW; wave++)
+            for (int r = 0; r < R; r++)
+                for (int lane = 0; lane < 64; lane++) {
+                    const int i0 = g1_red_row(k, wave, R, r) + 2 * lane;
+                    if (i0 < 0 || i0 + 2 > ll.act) fail("red zeroing outside red");
+                }
+
+    // ---- activation table: tag of each occurrence (segment k, block) and rows written
+    std::vector<int> occ_k(w.nocc, -1), occ_blk(w.nocc, -1);
+    for (int wave = 0; wave < G1_NW; wave++)
+        for (int i = wave; i < w.nocc; i += G1_NW) {
+            int k, blk;
+            g1_occ_block(a, w, i, k, blk);
+            if (k < 0 || k >= w.nseg) fail("occurrence %d: segment %d of %d", i, k, w.nseg);
+            if (blk < 0 || blk >= ntr / 8) fail("occurrence %d: block %d of %d", i, blk, ntr / 8);
+            if (occ_k[i] >= 0) fail("occurrence %d written twice", i);
+            occ_k[i] = k;
+            occ_blk[i] = blk;
+            const int s = g1_shard_of_seg<ONE>(a, sht, w.S_first + k);
+            const int gi = shard_of(s);
+            const G1Shard& e = g1_sh<ONE>(sht, s);
+            for (int lane = 0; lane < 64; lane++) {
+                need_in(reinterpret_cast<const uint32_t*>(e.suh + blk * 128) + lane, 4, B_SUH + gi,
+                        (long)W.sh[gi].ic * 2, "suh load");
+                for (int r = 0; r < R; r++) {
+                    need_in(reinterpret_cast<const uint32_t*>(a.x + g1_x_elem(a, r, blk)) + lane, 4, B_X,
+                            (long)W.rows * ic * 2, "activation load");
+                    const int aw = g1_act_word(i, lane, R, r);
+                    if (aw < 0 || aw + 2 > ll.zero - ll.act) fail("act store outside act (word %d)", aw);
+                }
+            }
+        }
+
+    // ---- per wave: prefetch and processing cursors, LDS reads, flushes
+    std::vector<int> red_written((size_t)w.nseg * G1_NW, 0);
+    for (int wave = 0; wave < G1_NW; wave++) {
+        const G1Run run = g1_wave_run(w.L, wave);
+        const int n = run.n;
+        if (n < 0 || run.lo < 0 || run.lo + n > w.L) fail("wave %d run [%d, +%d) of %d", wave, run.lo, n, w.L);
+        auto check_load = [&](const G1Cursor& q, const char* what) {
+            const int gi = shard_of(q.s);
+            const G1Shard& e = g1_sh<ONE>(sht, q.s);
+            if (q.cg < 0 || q.cg >= e.ncg || q.tr < 0 || q.tr >= ntr)
+                fail("%s: cursor cg %d tr %d (ncg %d, ntr %d)", what, q.cg, q.tr, e.ncg, ntr);
+            if (q.p != e.trellis + ((long)q.tr * e.oc16 + 8 * q.cg) * (8 * K))
+                fail("%s: cursor pointer does not match its tile row", what);
+            for (int lane = 0; lane < 64; lane++)
+                need_in(q.p + g1_lane_word(lane, K), 4L * K, B_TRELLIS + gi, trellis_words(gi) * 4, what);
+            W.loads++;
+        };
+        G1Cursor pf = g1_cursor_at<K, ONE>(a, sht, w.ub + run.lo), cu = pf;
+        int jpf = 0;
+        constexpr int D = g1_depth(K);
+        if (n > 0) {
+            check_load(pf, "first trellis load");
+            for (int d = 1; d < D; d++) {
+                g1_next_pf<K, ONE>(a, sht, pf, jpf, n);
+                check_load(pf, "prefetch");
+            }
+        }
+        int cur = cu.S - w.S_first;
+        int occ = g1_occ_of(w, cur, cu.tr);
+        auto flush = [&](int k) {
+            if (cur < 0 || cur >= w.nseg) fail("flush of segment %d of %d", cur, w.nseg);
+            for (int lane = 0; lane < 64; lane++) {
+                const int yrow = g1_yrow(lane), ycol = g1_ycol(lane);
+                if (yrow >= R) continue;
+                const int base = g1_red_row(cur, wave, R, yrow) + ycol;
+                for (int e = 0; e < 4; e++)
+                    if (base + 32 * e + 8 >= ll.act || base + 32 * e < 0) fail("flush outside red");
+            }
+            red_written[(size_t)cur * G1_NW + wave]++;
+            cur = k;
+        };
+        for (int j = 0; j < n; j += D)
+            for (int d = 0; d < D; d++) {
+                if (d == 0 || j + d < n) {
+                    if (cu.S - w.S_first != cur) flush(cu.S - w.S_first);
+                    // the unit this iteration decodes
+                    const int gi = shard_of(cu.s);
+                    const G1Shard& e = g1_sh<ONE>(sht, cu.s);
+                    if (cu.S != e.sbeg + cu.cg) fail("cursor segment %d != shard segment %d", cu.S, e.sbeg + cu.cg);
+                    const long uid = W.unit_base[gi] + (long)cu.cg * ntr + cu.tr;
+                    if (W.unit_seen[uid]++) fail("unit (shard %d, cg %d, tr %d) decoded twice", gi, cu.cg, cu.tr);
+                    // A operand: act entry of (occ, tr) or the zero operand, 64 bytes per lane
+                    if (occ < 0 || occ >= w.nocc) fail("occurrence %d of %d", occ, w.nocc);
+                    if (occ_k[occ] != cur || occ_blk[occ] != (cu.tr >> 3))
+                        fail("unit (seg %d, tr %d) reads occurrence %d = (seg %d, block %d)", cur, cu.tr, occ,
+                             occ_k[occ], occ_blk[occ]);
+                    const uint32_t ent = g1_a_entry(occ, cu.tr, R);
+                    for (int lane = 0; lane < 64; lane++) {
+                        const uint32_t asel = g1_asel(lane), aoff = g1_aoff(lane, R, ll);
+                        const uint32_t byte = ent * asel + aoff;
+                        if (asel) {
+                            if (byte < 4u * ll.act || byte + 64 > 4u * ll.zero) fail("A read outside act");
+                            // it must be the table row (occurrence, tile row, activation row)
+                            const uint32_t rel = (byte - 4u * ll.act) / 64;
+                            const int want_r = std::min((lane & 15) >> 2, R - 1);
+                            if (rel != (uint32_t)((occ * 8 + (cu.tr & 7)) * R + want_r)) fail("A read of a wrong table row");
+                        } else if (byte != 4u * ll.zero) {
+                            fail("zero-operand lane reads byte %u, not the zero words", byte);
+                        }
+                        if (byte + 64 > 4u * ll.words) fail("A read beyond the LDS layout");
+                    }
+                    W.lds_reads++;
+                    if (j + d + 1 < n) {
+                        g1_advance<K, ONE>(a, sht, cu);
+                        occ += (cu.tr & 7) == 0;
+                    }
+                }
+                g1_next_pf<K, ONE>(a, sht, pf, jpf, n);
+                check_load(pf, "trellis load");
+            }
+        if (n > 0) flush(cur);
+    }
+
+    // ---- tail: per segment, finish here or store the slot
+    const int nr = R == 1 ? 1 : a.nrows;
+    for (int wave = 0; wave < G1_NW; wave++)
+        for (int k = wave; k < w.nseg; k += G1_NW) {
+            for (int r = 0; r < R; r++)
+                for (int ww = 0; ww < G1_NW; ww++)
+                    if (g1_red_row(k, ww, R, r) + 128 > ll.act) fail("red read outside red");
+            const int S = w.S_first + k;
+            int g_lo, g_hi;
+            g1_contributors<ONE>(a, sht, S, g_lo, g_hi);
+            if (g < g_lo || g > g_hi) fail("wg %d holds segment %d but contributors are %d..%d", g, S, g_lo, g_hi);
+            const int s = g1_shard_of_seg<ONE>(a, sht, S);
+            const int gi = shard_of(s);
+            const G1Shard& e = g1_sh<ONE>(sht, s);
+            const int cg = S - e.sbeg;
+            if (cg < 0 || cg >= e.ncg) fail("segment %d: column group %d of %d", S, cg, e.ncg);
+            if (g_hi > g_lo) {
+                const float* base = a.slots + g1_slot(S, g, R);
+                for (int r = 0; r < R; r++) {
+                    const uint64_t* row = reinterpret_cast<const uint64_t*>(base) + g1_slot_word(0, R, r);
+                    need_in(row, 64 * 8, B_SLOTS, (long)W.slot_bytes, "slot store");
+                    need_in(row, 64 * 8, B_SLOTS, off_of(a.slots) + (long)(a.G + a.nsegs) * R * 128 * 4,
+                            "slot store (group share)");
+                    if (off_of(row) < off_of(a.slots)) fail("slot store before the group's share");
+                    auto it = W.slot_rows.find(off_of(row));
+                    if (it != W.slot_rows.end()) fail("slot row written twice (segment %d, wg %d, row %d)", S, g, r);
+                    W.slot_rows[off_of(row)] = std::make_tuple(launch * 1000000 + S, g, r);
+                }
+            } else {
+                for (int r = 0; r < nr; r++)
+                    for (int lane = 0; lane < 64; lane++) {
+                        need_in(reinterpret_cast<const uint32_t*>(e.svh + cg * 128) + lane, 4, B_SVH + gi,
+                                (long)W.sh[gi].oc * 2, "svh load");
+                        const uint16_t* o = e.C + r * e.ldc + cg * 128 + 2 * lane;
+                        need_in(o, 4, B_C, (long)W.rows * W.ldc * 2, "output store");
+                        const long el = off_of(o) / 2;
+                        const long col = el % W.ldc, row = el / W.ldc;
+                        if (row != r || col < W.col0[gi] || col + 2 > W.col0[gi] + W.sh[gi].oc)
+                            fail("output store at row %ld column %ld outside shard %d", row, col, gi);
+                        W.out[el]++;
+                        W.out[el + 1]++;
+                    }
+            }
+        }
+}
+
+template <bool ONE, int R>
+void g1_replay_wg_k(int K, G1World& W, const GemvShard* shards, const G1Group& a, const G1Shard* sht, int g,
+                    size_t lds, int launch)
+{
+    switch (K) {
+    case 1: g1_replay_wg<1, ONE, R>(W, shards, a, sht, g, lds, launch); break;
+    case 2: g1_replay_wg<2, ONE, R>(W, shards, a, sht, g, lds, launch); break;
+    case 3: g1_replay_wg<3, ONE, R>(W, shards, a, sht, g, lds, launch); break;
+    case 4: g1_replay_wg<4, ONE, R>(W, shards, a, sht, g, lds, launch); break;
+    case 5: g1_replay_wg<5, ONE, R>(W, shards, a, sht, g, lds, launch); break;
+    case 6: g1_replay_wg<6, ONE, R>(W, shards, a, sht, g, lds, launch); break;
+    case 7: g1_replay_wg<7, ONE, R>(W, shards, a, sht, g, lds, launch); break;
+    case 8: g1_replay_wg<8, ONE, R>(W, shards, a, sht, g, lds, launch); break;
+    default: fail("K=%d", K);
+    }
+}
+
+void g1_replay_group(G1World& W, const GemvShard* shards, int K, bool one, int R, const G1Group& a,
+                     const G1Shard* sht, int g, size_t lds, int launch)
+{
+    if (one) {
+        if (R == 1) g1_replay_wg_k<true, 1>(K, W, shards, a, sht, g, lds, launch);
+        else g1_replay_wg_k<true, G1_ROWS>(K, W, shards, a, sht, g, lds, launch);
+    } else {
+        if (R == 1) g1_replay_wg_k<false, 1>(K, W, shards, a, sht, g, lds, launch);
+        else g1_replay_wg_k<false, G1_ROWS>(K, W, shards, a, sht, g, lds, launch);
+    }
+}
+
+// gemv1_finish_kernel / gemv1_finish_multi_kernel for segment S of group a.
+template <bool ONE>
+void g1_replay_finish(G1World& W, const GemvShard* shards, int R, const G1Group& a, const G1Shard* sht, int S,
+                      int launch)
+{
+    if (S >= a.nsegs) return;
+    const int s = g1_shard_of_seg<ONE>(a, sht, S);
+    if (s < 0 || s >= a.nshards) fail("finish: shard %d", s);
+    const G1Shard& e = g1_sh<ONE>(sht, s);
+    const int gi = shard_index(W, shards, e.trellis);
+    const int cg = S - e.sbeg;
+    if (cg < 0 || cg >= e.ncg) fail("finish: column group %d of %d", cg, e.ncg);
+    int g_lo, g_hi;
+    g1_contributors<ONE>(a, sht, S, g_lo, g_hi);
+    if (g_hi == g_lo) return;
+    if (g_lo < 0 || g_hi >= a.G) fail("finish: contributors %d..%d of %d", g_lo, g_hi, a.G);
+    const int nsl = g_hi - g_lo + 1;
+    const int nr = R == 1 ? 1 : a.nrows;
+    const uint64_t* sl = reinterpret_cast<const uint64_t*>(a.slots + g1_slot(S, g_lo, R));
+    constexpr int B = 32;
+    for (int r = 0; r < nr; r++) {
+        for (int t0 = 0; t0 < nsl; t0 += B)
+            for (int t = 0; t < B; t++) {
+                const int tt = std::min(t0 + t, nsl - 1);
+                const uint64_t* row = sl + g1_slot_word(tt, R, r);
+                need_in(row, 64 * 8, B_SLOTS, (long)W.slot_bytes, "slot load");
+                auto it = W.slot_rows.find(off_of(row));
+                if (it == W.slot_rows.end()) fail("finish reads a slot row nobody wrote (segment %d, wg %d)", S, g_lo + tt);
+                if (it->second != std::make_tuple(launch * 1000000 + S, g_lo + tt, r))
+                    fail("finish of segment %d reads the slot row of another (segment, wg, row)", S);
+            }
+        for (int lane = 0; lane < 64; lane++) {
+            need_in(reinterpret_cast<const uint32_t*>(e.svh + cg * 128) + lane, 4, B_SVH + gi, (long)W.sh[gi].oc * 2,
+                    "svh load (finish)");
+            const uint16_t* o = e.C + r * e.ldc + cg * 128 + 2 * lane;
+            need_in(o, 4, B_C, (long)W.rows * W.ldc * 2, "output store (finish)");
+            const long el = off_of(o) / 2;
+            W.out[el]++;
+            W.out[el + 1]++;
+        }
+    }
+}
+
+int g1_replay(G1World& W, const GemvShard* shards, int nshards, int cus, long long* stats)
+{
+    int launch = 0;
+    const int rc = g1_plan(fake_ptr<uint16_t>(B_X), shards, nshards, W.rows, fake_ptr<char>(B_SLOTS), W.slot_bytes, cus,
+                           [&](const G1Launch& L) {
+        if (L.lds > 160 * 1024) fail("launch %d: %zu bytes of LDS per workgroup", launch, L.lds);
+        if (L.G < 1 || L.G > G1_GMAX * G1_MAXSH) fail("launch %d: %d workgroups", launch, L.G);
+        bool any_split = false;
+        // split segments by plain division (independent of the magic-number divisions)
+        auto note_split = [&](const G1Group& a) {
+            const long big = (long)a.r * (a.q + 1);
+            auto wg_of = [&](long u) { return u < big ? u / (a.q + 1) : a.r + (u - big) / a.q; };
+            for (int S = 0; S < a.nsegs; S++)
+                any_split = any_split || wg_of((long)S * a.ntr + a.ntr - 1) > wg_of((long)S * a.ntr);
+        };
+        if (!L.multi) {
+            const G1Group& a = L.args->grp;
+            if (a.G != L.G) fail("launch %d: group G %d != launch G %d", launch, a.G, L.G);
+            note_split(a);
+            for (int g = 0; g < L.G; g++) g1_replay_group(W, shards, L.K, L.one, L.R, a, L.args->sh, g, L.lds, launch);
+            if (L.finish) {
+                if (L.fblocks != a.nsegs) fail("finish blocks %d != segments %d", L.fblocks, a.nsegs);
+                for (int S = 0; S < L.fblocks; S++) {
+                    if (L.one) g1_replay_finish<true>(W, shards, L.R, a, L.args->sh, S, launch);
+                    else g1_replay_finish<false>(W, shards, L.R, a, L.args->sh, S, launch);
+                }
+            }
+        } else {
+            const G1Multi& m = *L.m;
+            for (int t = 0; t < m.ngrp; t++) note_split(m.grp[t]);
+            for (int b = 0; b < L.G; b++) {
+                const int i = g1_group_of(m.gbeg, m.ngrp, b);
+                const int g = b - m.gbeg[i];
+                if (g < 0 || g >= m.grp[i].G) fail("multi launch: block %d -> group %d wg %d of %d", b, i, g, m.grp[i].G);
+                g1_replay_group(W, shards, m.K[i], false, L.R, m.grp[i], m.sh + m.sh0[i], g, L.lds, launch);
+            }
+            if (L.finish)
+                for (int b = 0; b < L.fblocks; b++) {
+                    const int i = g1_group_of(m.fbeg, m.ngrp, b);
+                    g1_replay_finish<false>(W, shards, L.R, m.grp[i], m.sh + m.sh0[i], b - m.fbeg[i], launch);
+                }
+        }
+        if (any_split != L.finish) fail("launch %d: finish kernel %d but split segments %d", launch, L.finish, any_split);
+        launch++;
+        return EXL3_OK;
+    });
+    if (rc != EXL3_OK) fail("plan refused: %s", g_err);
+    for (size_t u = 0; u < W.unit_seen.size(); u++)
+        if (W.unit_seen[u] != 1) fail("unit %zu decoded %d times", u, W.unit_seen[u]);
+    for (int r = 0; r < W.rows; r++)
+        for (size_t gi = 0; gi < W.sh.size(); gi++)
+            for (int c = 0; c < W.sh[gi].oc; c++) {
+                const uint8_t n = W.out[(size_t)r * W.ldc + W.col0[gi] + c];
+                if (n != 1) fail("output row %d shard %zu column %d written %d times", r, gi, c, n);
+            }
+    if (stats) {
+        stats[0] = launch;
+        stats[1] = W.loads;
+        stats[2] = W.lds_reads;
+        stats[3] = (long long)W.slot_rows.size();
+    }
+    return 0;
+}
+
+
+// ================================================================ stream-K GEMM
+
+struct SkWorld {
+    int rows, ic;
+    std::vector<ShardSpec> sh;
+    std::vector<int> col0;
+    long ldc;
+    size_t ws_bytes;
+    std::vector<uint8_t> out;
+    std::vector<std::pair<long, long>> ws_regions;   // [begin, end) of each workspace use
+    std::vector<int> ah_buf;                          // Ah of shard i: B_AH + i (single) or B_WS
+    long loads = 0, pieces = 0, slot_writes = 0;
+};
+
+void ws_region(SkWorld& W, const void* p, long bytes, const char* what)
+{
+    need_in(p, bytes, B_WS, (long)W.ws_bytes, what);
+    const long b = off_of(p), e = b + bytes;
+    for (auto& r : W.ws_regions)
+        if (b < r.second && r.first < e) fail("%s: workspace bytes [%ld, %ld) overlap [%ld, %ld)", what, b, e, r.first, r.second);
+    W.ws_regions.push_back({b, e});
+}
+
+int sk_shard_index(const SkWorld& W, const GemvShard* shards, const uint32_t* trellis)
+{
+    for (size_t i = 0; i < W.sh.size(); i++)
+        if (shards[i].trellis == trellis) return (int)i;
+    return -1;
+}
+
+// The LDS tiles of a BM-row launch: every A / B element the MFMAs read is one a store wrote,
+// and all accesses stay in their buffer's tile (independent of the piece, so checked once).
+template <int BM, int NBUF>
+void sk_check_lds()
+{
+    constexpr int MB = SkCfg<BM>::MB, NB = SkCfg<BM>::NB, AP = (BM + 63) / 64;
+    const int lds_halves = sk_lds<BM, NBUF>() / 2;
+    for (int b = 0; b < NBUF; b++) {
+        std::vector<uint8_t> aw((size_t)BM * SK_KS, 0), bw((size_t)SK_BN * SK_KS, 0);
+        for (int tid = 0; tid < 64 * SK_WAVES; tid++) {
+            const int arow = sk_arow(tid), aseg = sk_aseg(tid);
+            for (int p = 0; p < AP; p++) {
+                if (!sk_apass<BM>(p, arow)) continue;
+                const int i = sk_a_store(p, arow, aseg);
+                const int row = i / SK_LD, col = i % SK_LD;
+                if (row >= BM || col + 8 > SK_KS) fail("A store outside the A tile (BM %d)", BM);
+                if (sk_as<BM>(b) + i + 8 > sk_bs<BM>(b)) fail("A store into the B tile");
+                for (int e = 0; e < 8; e++) aw[(size_t)row * SK_KS + col + e]++;
+            }
+            for (int j = 0; j < 4; j++) {
+                const int i = sk_b_store(sk_bn0(tid), sk_bk0(tid), j);
+                const int row = i / SK_LD, col = i % SK_LD;
+                if (row >= SK_BN || col + 8 > SK_KS) fail("B store outside the B tile");
+                if (sk_bs<BM>(b) + i + 8 > lds_halves) fail("B store beyond LDS");
+                for (int e = 0; e < 8; e++) bw[(size_t)row * SK_KS + col + e]++;
+            }
+        }
+        for (size_t i = 0; i < aw.size(); i++)
+            if (aw[i] != 1) fail("A tile element %zu stored %d times (BM %d)", i, aw[i], BM);
+        for (size_t i = 0; i < bw.size(); i++)
+            if (bw[i] != 1) fail("B tile element %zu stored %d times", i, bw[i]);
+        for (int wave = 0; wave < SK_WAVES; wave++) {
+            const int wm = wave / SkCfg<BM>::WN, wn = wave % SkCfg<BM>::WN;
+            for (int lane = 0; lane < 64; lane++)
+                for (int h = 0; h < 2; h++) {
+                    for (int nb = 0; nb < NB; nb++) {
+                        const int i = sk_b_frag<BM>(wn, nb, lane, h);
+                        if (i / SK_LD >= SK_BN || i % SK_LD + 8 > SK_KS) fail("B fragment outside the B tile");
+                    }
+                    for (int mb = 0; mb < MB; mb++) {
+                        const int i = sk_a_frag<BM>(wm, mb, lane, h);
+                        if (i / SK_LD >= BM || i % SK_LD + 8 > SK_KS) fail("A fragment outside the A tile (BM %d)", BM);
+                    }
+                }
+        }
+    }
+    // epilogue staging
+    const int lds_floats = sk_lds<BM, NBUF>() / 4;
+    for (int wave = 0; wave < SK_WAVES; wave++) {
+        const int wm = wave / SkCfg<BM>::WN, wn = wave % SkCfg<BM>::WN;
+        for (int lane = 0; lane < 64; lane++)
+            for (int nb = 0; nb < NB; nb++)
+                for (int e = 0; e < 4; e++) {
+                    int i;
+                    if (BM == 256) i = sk_c256(wm, wn >> 1, 4 * (lane >> 4) + e, 64 * (wn & 1) + 16 * nb + (lane & 15));
+                    else i = sk_cx(4 * (lane >> 4) + e, NB * 16 * wn + 16 * nb + (lane & 15));
+                    if (i < 0 || i >= lds_floats) fail("epilogue staging store beyond LDS (BM %d)", BM);
+                }
+    }
+}
+
+// One BM-row launch (after the clear or set-up kernel): every workgroup's pieces, their loads,
+// slot traffic and epilogue stores.
+template <int BM, int NBUF>
+void sk_replay_launch(SkWorld& W, const GemvShard* shards, const SkLaunch& L, int launch)
+{
+    constexpr int MB = SkCfg<BM>::MB, NB = SkCfg<BM>::NB, AP = (BM + 63) / 64;
+    const SkArgs& a = *L.args;
+    const int G = L.G;
+    const long units = (long)a.ntiles * a.nks;
+    if (G < 1) fail("launch %d: %d workgroups", launch, G);
+    if (sk_first(a, G) != units) fail("launch %d: ranges end at %ld, not %ld", launch, sk_first(a, G), units);
+    if (a.q < 1) fail("launch %d: %d K-steps per workgroup", launch, a.q);
+    sk_check_lds<BM, NBUF>();
+    // counters and slots inside the workspace share of this launch
+    ws_region(W, a.counters, (long)a.ntiles * 4, "tile counters");
+    const long slot_floats = (long)(a.ntiles + G) * SK_WAVES * sk_acc<BM>() * 64;
+    ws_region(W, a.slots, slot_floats * 4, "slots");
+    if (off_of(a.slots) < off_of(a.counters) + (long)a.ntiles * 4) fail("slots before the counters end");
+
+    std::vector<int> seen_g(G, 0);
+    std::vector<int> partial(a.ntiles, 0);
+    std::vector<int> tile_done(a.ntiles, 0);
+    std::map<std::tuple<int, int>, int> slot_by;   // (tile, g) -> waves written
+
+    auto epilogue = [&](int t) {
+        int si = 0;
+        for (int i = 1; i < SK_MAXSH; i++)
+            if (i < a.nshards && t >= a.sh[i].tbeg) si = i;
+        const SkShard& S = a.sh[si];
+        const int gi = sk_shard_index(W, shards, S.trellis);
+        const int tl = t - S.tbeg, tm = tl / S.ntn, tn = tl - tm * S.ntn, m0 = tm * BM, tc = S.oc >> 4;
+        auto store_row = [&](int row, int ob, int lane) {
+            if (!(ob < tc && row < a.rows)) return;
+            need_in(reinterpret_cast<const uint32_t*>(S.svh + ob * 16) + lane, 4, B_SVH + gi, (long)W.sh[gi].oc * 2,
+                    "svh load");
+            const uint16_t* o = S.C + (long)row * S.ldc + ob * 16 + 2 * lane;
+            need_in(o, 4, B_C, (long)W.rows * W.ldc * 2, "output store");
+            const long el = off_of(o) / 2;
+            const long col = el % W.ldc;
+            if (el / W.ldc != row || col < W.col0[gi] || col + 2 > W.col0[gi] + W.sh[gi].oc)
+                fail("output (%d, %ld) outside shard %d", row, col, gi);
+            W.out[el]++;
+            W.out[el + 1]++;
+        };
+        for (int wave = 0; wave < SK_WAVES; wave++) {
+            const int wm = wave / SkCfg<BM>::WN, wn = wave % SkCfg<BM>::WN;
+            for (int lane = 0; lane < 64; lane++) {
+                if (BM == 256) {
+                    const int blk = wn >> 1, half = wn & 1;
+                    for (int mb = 0; mb < MB; mb++)
+                        for (int r = 8 * half; r < 8 * half + 8; r++)
+                            store_row(m0 + 128 * wm + 16 * mb + r, 16 * tn + 8 * blk, lane);
+                } else {
+                    for (int mb = 0; mb < MB; mb++)
+                        for (int jj = 0; jj < 4; jj++) {
+                            const int j = wave + SK_WAVES * jj;
+                            store_row(m0 + 16 * mb + (j & 15), 16 * tn + 8 * (j >> 4), lane);
+                        }
+                }
+            }
+        }
+        tile_done[t]++;
+    };
+
+    for (int b = 0; b < G; b++) {
+        const int g = sk_logical(b, G);
+        if (g < 0 || g >= G || seen_g[g]++) fail("launch %d: slot %d maps to logical workgroup %d twice/outside", launch, b, g);
+        const long u_begin = sk_first(a, g), u_end = sk_first(a, g + 1);
+        if (u_end - u_begin < 1) fail("launch %d: workgroup %d has no K-steps", launch, g);
+        long u = u_begin;
+        while (u < u_end) {
+            const SkPiece pc = sk_piece<BM>(a, u, u_end);
+            if (pc.t < 0 || pc.t >= a.ntiles) fail("piece tile %d of %d", pc.t, a.ntiles);
+            if (pc.si < 0 || pc.si >= a.nshards) fail("piece shard %d", pc.si);
+            if (!(0 <= pc.s0 && pc.s0 < pc.s1 && pc.s1 <= a.nks)) fail("piece steps %d..%d of %d", pc.s0, pc.s1, a.nks);
+            const SkShard& S = a.sh[pc.si];
+            const int gi = sk_shard_index(W, shards, S.trellis);
+            const int nrb = (a.rows + BM - 1) / BM;
+            if (pc.tm >= nrb || pc.tn >= S.ntn || pc.t - S.tbeg >= nrb * S.ntn) fail("piece tile (%d, %d) outside shard", pc.tm, pc.tn);
+            const int KK = L.K > 0 ? L.K : S.K;
+            if (KK != W.sh[gi].K) fail("piece decodes K=%d, shard has K=%d", KK, W.sh[gi].K);
+            const long twords = (long)(W.sh[gi].ic / 16) * (W.sh[gi].oc / 16) * 8 * KK;
+            auto load_step = [&](int s) {
+                if (s < pc.s0 || s >= pc.s1) fail("K-step %d loaded outside the piece %d..%d", s, pc.s0, pc.s1);
+                for (int tid = 0; tid < 64 * SK_WAVES; tid++) {
+                    const int arow = sk_arow(tid), aseg = sk_aseg(tid);
+                    for (int p = 0; p < AP; p++) {
+                        const int row = pc.m0 + 64 * p + arow;
+                        if (sk_apass<BM>(p, arow) && row < a.rows) {
+                            const long el = sk_a_elem(a, row, s, aseg);
+                            need_in(S.Ah + el, 16, W.ah_buf[gi] >= 0 ? W.ah_buf[gi] : B_WS,
+                                    W.ah_buf[gi] >= 0 ? (long)a.rows * a.ic * 2 : (long)W.ws_bytes, "A tile load");
+                            // the 8 halves are row `row`, inside K-step s's 64 columns
+                            if (el / a.ic != row || el % a.ic < (long)s * SK_KS || el % a.ic + 8 > (long)(s + 1) * SK_KS)
+                                fail("A tile load of row %d K-step %d reads row %ld column %ld", row, s, el / a.ic, el % a.ic);
+                        }
+                    }
+                    const int btn = sk_btn(tid, pc.tn);
+                    if (btn < pc.tc) {
+                        const long wd = sk_b_word(sk_bti(tid, s), pc.tc, sk_bcol(btn, pc.tc), tid & 7, KK);
+                        need_in(S.trellis + wd, 4L * KK, B_TRELLIS + gi, twords * 4, "trellis load");
+                        // one chunk of one tile: a tile row of K-step s, a tile column of block tn
+                        const long tile = wd / (8 * KK), ti = tile / pc.tc, tj = tile % pc.tc;
+                        if (wd % (8 * KK) + KK > 8 * KK || ti < 4L * s || ti >= 4L * s + 4 || tj < 16L * pc.tn ||
+                            tj >= 16L * pc.tn + 16)
+                            fail("trellis load of K-step %d, column block %d reads tile (%ld, %ld)", s, pc.tn, ti, tj);
+                    }
+                }
+                W.loads++;
+            };
+            // the kernel's load order
+            load_step(pc.s0);
+            if (NBUF == 2) {
+                load_step(std::min(pc.s0 + 1, pc.s1 - 1));
+                for (int st = pc.s0; st < pc.s1; st++) load_step(std::min(st + 2, pc.s1 - 1));
+            } else {
+                for (int st = pc.s0; st < pc.s1; st++)
+                    if (st + 1 < pc.s1) load_step(st + 1);
+            }
+            W.pieces++;
+            u += pc.s1 - pc.s0;
+            if (pc.s0 == 0 && pc.s1 == a.nks) {
+                epilogue(pc.t);
+                continue;
+            }
+            const int g_lo = sk_wg_of(a, (long)pc.t * a.nks), g_hi = sk_wg_of(a, (long)(pc.t + 1) * a.nks - 1);
+            if (g < g_lo || g > g_hi) fail("workgroup %d holds a piece of tile %d (contributors %d..%d)", g, pc.t, g_lo, g_hi);
+            for (int wave = 0; wave < SK_WAVES; wave++)
+                for (int i = 0; i < MB * NB * 2; i++) {
+                    const uint64_t* wp = reinterpret_cast<const uint64_t*>(a.slots + sk_slot<BM>(pc.t, g, wave)) + (long)i * 64;
+                    need_in(wp, 64 * 8, B_WS, off_of(a.slots) + slot_floats * 4, "slot store");
+                    if (off_of(wp) < off_of(a.slots)) fail("slot store before the slot area");
+                }
+            if (slot_by[{pc.t, g}]++) fail("tile %d: workgroup %d stores its slot twice", pc.t, g);
+            W.slot_writes++;
+            partial[pc.t]++;
+        }
+    }
+    // the last arriver of each split tile: counter reaches g_hi - g_lo, slots g_lo..g_hi read
+    for (int t = 0; t < a.ntiles; t++) {
+        if (!partial[t]) continue;
+        const int g_lo = sk_wg_of(a, (long)t * a.nks), g_hi = sk_wg_of(a, (long)(t + 1) * a.nks - 1);
+        if (partial[t] != g_hi - g_lo + 1) fail("tile %d: %d partial pieces, %d contributors", t, partial[t], g_hi - g_lo + 1);
+        for (int gg = g_lo; gg <= g_hi; gg++) {
+            if (!slot_by.count({t, gg})) fail("tile %d: slot of workgroup %d read but never written", t, gg);
+            // slots of distinct (tile, workgroup) pairs must not overlap: index t + gg is unique
+            // per pair only if no other tile's contributor shares it
+            for (int wave = 0; wave < SK_WAVES; wave++)
+                need_in(a.slots + sk_slot<BM>(t, gg, wave), (long)sk_acc<BM>() * 64 * 4, B_WS,
+                        off_of(a.slots) + slot_floats * 4, "slot load");
+        }
+        epilogue(t);
+    }
+    // distinct slot indices t + g across all written pairs
+    std::map<long, int> by_index;
+    for (auto& kv : slot_by)
+        if (by_index[std::get<0>(kv.first) + std::get<1>(kv.first)]++) fail("two (tile, workgroup) pairs share slot %d", std::get<0>(kv.first) + std::get<1>(kv.first));
+    for (int t = 0; t < a.ntiles; t++)
+        if (tile_done[t] != 1) fail("tile %d finished %d times", t, tile_done[t]);
+}
+
+void sk_replay_prep(SkWorld& W, const GemvShard* shards, const SkLaunch& L)
+{
+    const SkPrepArgs& p = *L.prep_args;
+    const long waves = 4 * ((L.prep_waves + 3) / 4);
+    for (int s = 0; s < p.nsh; s++) {
+        ws_region(W, p.Ah[s], (long)p.rows * p.ic * 2, "Ah");
+        if (p.Ah[s] != L.args->sh[s].Ah) fail("set-up and launch disagree on shard %d's Ah", s);
+    }
+    for (long w = 0; w < waves; w++) {
+        if (w < p.ntiles) need_in(p.counters + w, 4, B_WS, (long)W.ws_bytes, "counter clear");
+        if (w >= (long)p.nsh * p.rows * p.nblk) continue;
+        int s, r, b;
+        sk_prep_wave(p, (int)w, s, r, b);
+        if (s < 0 || s >= p.nsh || r >= p.rows || b >= p.nblk) fail("set-up wave %ld -> (%d, %d, %d)", w, s, r, b);
+        const int gi = sk_shard_index(W, shards, L.args->sh[s].trellis);
+        const long off = sk_prep_elem(p, r, b);
+        for (int lane = 0; lane < 64; lane++) {
+            need_in(reinterpret_cast<const uint32_t*>(p.A + off) + lane, 4, B_X, (long)W.rows * W.ic * 2, "A load (set-up)");
+            need_in(reinterpret_cast<const uint32_t*>(p.suh[s] + b * 128) + lane, 4, B_SUH + gi, (long)W.ic * 2, "suh load");
+            need_in(reinterpret_cast<const uint32_t*>(p.Ah[s] + off) + lane, 4, B_WS, (long)W.ws_bytes, "Ah store");
+            if (off_of(p.Ah[s] + off) + 4L * (lane + 1) > off_of(p.Ah[s]) + (long)p.rows * p.ic * 2) fail("Ah store past the shard's Ah");
+        }
+    }
+    if ((long)p.ntiles > waves) fail("set-up grid clears %ld of %d counters", waves, p.ntiles);
+}
+
+void sk_replay_any(SkWorld& W, const GemvShard* shards, const SkLaunch& L, int launch)
+{
+    if (L.prep) sk_replay_prep(W, shards, L);
+    switch (L.BM) {
+    case 16:
+        if (L.NBUF == 2) sk_replay_launch<16, 2>(W, shards, L, launch);
+        else sk_replay_launch<16, 1>(W, shards, L, launch);
+        break;
+    case 32: sk_replay_launch<32, 2>(W, shards, L, launch); break;
+    case 48: sk_replay_launch<48, 2>(W, shards, L, launch); break;
+    case 64: sk_replay_launch<64, 2>(W, shards, L, launch); break;
+    case 96: sk_replay_launch<96, 2>(W, shards, L, launch); break;
+    case 128: sk_replay_launch<128, 2>(W, shards, L, launch); break;
+    case 256: sk_replay_launch<256, 2>(W, shards, L, launch); break;
+    default: fail("tile height %d", L.BM);
+    }
+    if (L.K == 0 && !sk_has_k0<256>() && L.BM == 256) fail("per-shard-K launch of 256-row tiles");
+}
+
+}  // namespace
+
+extern "C" {
+
+// Message of the last failed replay ("" after a clean one).
+const char* exl3r_message() { return g_msg.c_str(); }
+
+// The 1..4-row GEMV (exl3_gemv with rows <= 4 on the gemv1 path) of nshards shards that share
+// ic, on a device with `cus` CUs.  concat != 0: the shards write adjacent column ranges of one
+// (rows, sum oc) output, as the grouped op does; else each its own (rows, oc) output (checked
+// as one buffer with a column offset per shard, ldc = sum oc).  Returns 0 when every access is
+// in bounds and every coverage check holds, 1 on a violation, 2 if the plan refused the call
+// (exl3r_message says which).  stats (4 entries, may be null): launches, wave-unit loads
+// checked, unit LDS reads checked, slot rows written.
+int exl3r_gemv1(int rows, int ic, int nshards, const int* oc, const int* K, const int* cb, int cus, long long* stats)
+{
+    g_msg.clear();
+    try {
+        if (nshards < 1 || nshards > EXL3_MAX_SHARDS) fail("nshards %d", nshards);
+        G1World W;
+        W.rows = rows;
+        W.ic = ic;
+        std::vector<GemvShard> shards(nshards);
+        long cols = 0;
+        W.slot_bytes = 0;
+        for (int i = 0; i < nshards; i++) {
+            W.sh.push_back(ShardSpec{ic, oc[i], K[i], cb[i]});
+            W.col0.push_back((int)cols);
+            cols += oc[i];
+            W.slot_bytes += (g1_slot_bytes(oc[i], rows) + 255) & ~(size_t)255;
+        }
+        W.ldc = cols;
+        W.out.assign((size_t)rows * cols + 2, 0);
+        long ub = 0;
+        for (int i = 0; i < nshards; i++) {
+            GemvShard& d = shards[i];
+            d.trellis = fake_ptr<uint32_t>(B_TRELLIS + i);
+            d.suh = fake_ptr<uint16_t>(B_SUH + i);
+            d.svh = fake_ptr<uint16_t>(B_SVH + i);
+            d.C = fake_ptr<uint16_t>(B_C) + W.col0[i];
+            d.ic = ic;
+            d.oc = oc[i];
+            d.K = K[i];
+            d.cb = cb[i];
+            d.ldc = W.ldc;
+            W.unit_base.push_back(ub);
+            ub += (long)(oc[i] / 128) * (ic / 16);
+        }
+        W.unit_seen.assign(ub, 0);
+        return g1_replay(W, shards.data(), nshards, cus, stats);
+    } catch (const Fail& f) {
+        g_msg = f.what;
+        return g_msg.rfind("plan refused", 0) == 0 ? 2 : 1;
+    }
+}
+
+
+// The stream-K GEMM for nshards shards sharing ic: mode 0 = exl3_gemm (one shard, tile height
+// by rows), 1 = exl3_gemm_grouped (tile height by rows), 2 = exl3_gemv's 5..16-row path
+// (16-row tiles).  Workspaces are sized as the product sizes them for `cus` CUs.  Returns as
+// exl3r_gemv1; stats: launches, K-step loads checked, pieces, slot stores.
+int exl3r_gemm_sk(int mode, int rows, int ic, int nshards, const int* oc, const int* K, const int* cb, int cus,
+                  long long* stats)
+{
+    g_msg.clear();
+    try {
+        if (nshards < 1 || nshards > EXL3_MAX_SHARDS || (mode == 0 && nshards != 1)) fail("nshards %d", nshards);
+        SkWorld W;
+        W.rows = rows;
+        W.ic = ic;
+        std::vector<GemvShard> shards(nshards);
+        long cols = 0;
+        size_t ws = 0;
+        const int bm = mode == 2 ? 16 : gemm_sk_bm(rows);
+        for (int i = 0; i < nshards; i++) {
+            W.sh.push_back(ShardSpec{ic, oc[i], K[i], cb[i]});
+            W.col0.push_back((int)cols);
+            W.ah_buf.push_back(mode == 0 ? B_AH + i : -1);
+            cols += oc[i];
+            if (mode == 0) ws += sk_single_bytes(rows, oc[i], cus);
+            else if (mode == 1) ws += sk_grouped_bytes_bm(bm, rows, ic, oc[i], cus);
+            else ws += sk_align(sk_grouped_bytes<16>(rows, ic, oc[i], cus));
+        }
+        W.ldc = cols;
+        W.ws_bytes = ws;
+        W.out.assign((size_t)rows * cols + 2, 0);
+        for (int i = 0; i < nshards; i++) {
+            GemvShard& d = shards[i];
+            d.trellis = fake_ptr<uint32_t>(B_TRELLIS + i);
+            d.suh = fake_ptr<uint16_t>(B_SUH + i);
+            d.svh = fake_ptr<uint16_t>(B_SVH + i);
+            d.C = fake_ptr<uint16_t>(B_C) + W.col0[i];
+            d.ic = ic;
+            d.oc = oc[i];
+            d.K = K[i];
+            d.cb = cb[i];
+            d.ldc = W.ldc;
+        }
+        int launch = 0;
+        auto emit = [&](const SkLaunch& L) {
+            sk_replay_any(W, shards.data(), L, launch++);
+            return EXL3_OK;
+        };
+        int rc;
+        if (mode == 0) {
+            rc = sk_plan_single(fake_ptr<uint16_t>(B_AH), shards[0].trellis, shards[0].C, shards[0].svh, fake_ptr<char>(B_WS),
+                                ws, rows, ic, oc[0], K[0], cb[0], cus, emit);
+        } else {
+            const char* what = mode == 1 ? "exl3_gemm_grouped" : "exl3_gemv";
+            switch (bm) {
+            case 16: rc = sk_plan_grouped<16>(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, what, cus, emit); break;
+            case 32: rc = sk_plan_grouped<32>(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, what, cus, emit); break;
+            case 48: rc = sk_plan_grouped<48>(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, what, cus, emit); break;
+            case 64: rc = sk_plan_grouped<64>(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, what, cus, emit); break;
+            case 96: rc = sk_plan_grouped<96>(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, what, cus, emit); break;
+            case 128: rc = sk_plan_grouped<128>(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, what, cus, emit); break;
+            default: rc = sk_plan_grouped<256>(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, what, cus, emit); break;
+            }
+        }
+        if (rc != EXL3_OK) fail("plan refused: %s", exl3::g_err);
+        for (int r = 0; r < rows; r++)
+            for (int i = 0; i < nshards; i++)
+                for (int c = 0; c < oc[i]; c++) {
+                    const uint8_t n = W.out[(size_t)r * W.ldc + W.col0[i] + c];
+                    if (n != 1) fail("output row %d shard %d column %d written %d times", r, i, c, n);
+                }
+        if (stats) {
+            stats[0] = launch;
+            stats[1] = W.loads;
+            stats[2] = W.pieces;
+            stats[3] = W.slot_writes;
+        }
+        return 0;
+    } catch (const Fail& f) {
+        g_msg = f.what;
+        return g_msg.rfind("plan refused", 0) == 0 ? 2 : 1;
+    }
+}
+
+}  // extern "C"
