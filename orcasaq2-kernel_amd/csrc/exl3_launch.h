@@ -35,7 +35,7 @@ struct GemvShard {
 constexpr size_t GEMV_COUNTER_BYTES = 16384;
 size_t gemv_workspace_bytes(int rows, int ic, int oc);
 size_t gemv1_slot_bytes(int ic, int oc, int rows);
-bool gemv1_rows_fit(const GemvShard* shards, int nshards);
+bool gemv1_rows_fit(const GemvShard* shards, int nshards, int rows);
 int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
                    size_t slot_bytes, hipStream_t stream);
 int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows,

@@ -304,7 +304,7 @@ int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int r
                          offs[nshards]);
 
     char* ws = static_cast<char*>(workspace);
-    if (rows == 1 || (rows <= GV_SPLIT_MAX_ROWS && gemv1_rows_fit(shards, nshards)))
+    if (rows == 1 || (rows <= GV_SPLIT_MAX_ROWS && gemv1_rows_fit(shards, nshards, rows)))
         return gemv1_dispatch(A, shards, nshards, rows, ws + GEMV_COUNTER_BYTES, offs[nshards] - GEMV_COUNTER_BYTES,
                               stream);
     if (rows > GV_SPLIT_MAX_ROWS)

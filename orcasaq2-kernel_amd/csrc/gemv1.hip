@@ -127,6 +127,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     constexpr int D = g1_depth(K);
 
     const G1Range w = g1_range<ONE>(a, sht, g);
+    const int nr = R == 1 ? 1 : a.nrows;     // activation rows in the tables and results
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     __builtin_amdgcn_s_setprio(3);
@@ -152,32 +153,42 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     };
     Slot ring[D];
 
-    const G1Lds ll = g1_lds_layout(w.nseg, w.nocc, R);
+    const G1Lds ll = g1_lds_layout(w.nseg, w.nocc, nr);
     float* red = reinterpret_cast<float*>(lds);
     uint32_t* act = lds + ll.act;
     uint32_t* zero = lds + ll.zero;
     if (threadIdx.x < 16) zero[threadIdx.x] = 0u;
-    for (int k = 0; k < w.nseg; k++)
-#pragma unroll
-        for (int r = 0; r < R; r++)
-            *reinterpret_cast<float2*>(red + g1_red_row(k, wave, R, r) + 2 * lane) = float2{0.f, 0.f};
     const Dot2Consts kc = dot2_consts();
 
-    // Activations, once per workgroup: the waves share out the occurrences; each transforms
-    // its block of every activation row r, fp16(H128(x_r * suh)) (lane l: outputs 2l, 2l + 1
-    // = rows 2(l % 8), 2(l % 8) + 1 of the block's tile row l / 8) and stores each output as a
-    // duplicated fp16 pair in the order the MFMAs read them (g1_act_word).
-    for (int i = wave; i < w.nocc; i += G1_NW) {
-        int k, blk;
-        g1_occ_block(a, w, i, k, blk);
-        const int s = g1_shard_of_seg<ONE>(a, sht, w.S_first + k);
-        const uint32_t sw = reinterpret_cast<const uint32_t*>(sh(s).suh + blk * 128)[lane];
-#pragma unroll 1
-        for (int r = 0; r < R; r++) {
-            const uint32_t xw = reinterpret_cast<const uint32_t*>(a.x + g1_x_elem(a, r, blk))[lane];
-            float v0 = g1_lo(xw) * g1_lo(sw), v1 = g1_hi(xw) * g1_hi(sw);
-            wave_fwht128(v0, v1);
-            *reinterpret_cast<uint2*>(act + g1_act_word(i, lane, R, r)) = uint2{g1_dup(v0), g1_dup(v1)};
+    // Activations, once per workgroup: the waves share out the (occurrence, activation row)
+    // pairs; each transforms one block of one row, fp16(H128(x_r * suh)) (lane l: outputs 2l,
+    // 2l + 1 = rows 2(l % 8), 2(l % 8) + 1 of the block's tile row l / 8) and stores each
+    // output as a duplicated fp16 pair in the order the MFMAs read them (g1_act_word).  A wave
+    // issues the loads of up to G1_TBATCH of its pairs before transforming any of them.
+    const int ntask = w.nocc * nr;
+    for (int t0 = wave; t0 < ntask; t0 += G1_NW * G1_TBATCH) {
+        uint32_t sw[G1_TBATCH], xw[G1_TBATCH];
+#pragma unroll
+        for (int j = 0; j < G1_TBATCH; j++) {
+            const int t = t0 + j * G1_NW;
+            if (t < ntask) {
+                const int i = R == 1 ? t : t / nr, r = t - i * nr;
+                int k, blk;
+                g1_occ_block(a, w, i, k, blk);
+                const int s = g1_shard_of_seg<ONE>(a, sht, w.S_first + k);
+                sw[j] = reinterpret_cast<const uint32_t*>(sh(s).suh + blk * 128)[lane];
+                xw[j] = reinterpret_cast<const uint32_t*>(a.x + g1_x_elem(a, r, blk))[lane];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < G1_TBATCH; j++) {
+            const int t = t0 + j * G1_NW;
+            if (t < ntask) {
+                const int i = R == 1 ? t : t / nr, r = t - i * nr;
+                float v0 = g1_lo(xw[j]) * g1_lo(sw[j]), v1 = g1_hi(xw[j]) * g1_hi(sw[j]);
+                wave_fwht128(v0, v1);
+                *reinterpret_cast<uint2*>(act + g1_act_word(i, lane, nr, r)) = uint2{g1_dup(v0), g1_dup(v1)};
+            }
         }
     }
     // The first unit's loads go out after the wave's activation loads have returned, so those
@@ -197,17 +208,17 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     // steps whenever a unit starts a block (its tile row a multiple of 8, which includes
     // every segment start).
     // yacc[h][e] of lane 16r + n: activation row r's sum for output 32e + 16(n / 8) + n % 8 + 8h
-    // (lanes 16r + n with r >= R hold copies of row R - 1).
+    // (lanes 16r + n with r >= nr hold copies of row nr - 1).
     f32x4 yacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     const int yrow = g1_yrow(lane), ycol = g1_ycol(lane);
     const uint32_t asel = g1_asel(lane);
-    const uint32_t aoff = g1_aoff(lane, R, ll);
+    const uint32_t aoff = g1_aoff(lane, nr, ll);
     int cur = cu.S - w.S_first;
     int occ = g1_occ_of(w, cur, cu.tr);
     const int pq1 = (n + 3) >> 2, pq2 = (n + 1) >> 1, pq3 = (3 * n + 3) >> 2;
     auto flush = [&](int k) {
-        if (yrow < R) {
-            float* rr = red + g1_red_row(cur, wave, R, yrow) + ycol;
+        if (yrow < nr) {
+            float* rr = red + g1_red_row(cur, wave, nr, yrow) + ycol;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 rr[32 * e] = yacc[0][e];
@@ -222,7 +233,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         for (int d = 0; d < D; d++) {
             if (d == 0 || j + d < n) {
                 if (cu.S - w.S_first != cur) flush(cu.S - w.S_first);
-                const uint32_t e = g1_a_entry(occ, cu.tr, R);
+                const uint32_t e = g1_a_entry(occ, cu.tr, nr);
                 const f16x8* ap = reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(lds) + (__umul24(e, asel) + aoff));
                 const f16x8 av[4] = {ap[0], ap[1], ap[2], ap[3]};
                 chunk_prev_dpp<K>(ring[d].w, first_lane);
@@ -257,31 +268,30 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
                              ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v1) << 16);
         reinterpret_cast<uint32_t*>(sh(s).C + r * sh(s).ldc + cg * 128)[lane] = out;
     };
-    const int nr = R == 1 ? 1 : a.nrows;
-    for (int k = wave; k < w.nseg; k += G1_NW) {
-        float v0[R], v1[R];
+    // (segment, activation row) tasks shared out over the waves
+    for (int t = wave; t < w.nseg * nr; t += G1_NW) {
+        const int k = R == 1 ? t : t / nr, r = t - k * nr;
+        // the partial rows of the waves whose runs meet segment k, in wave order
+        int ub, ue;
+        g1_seg_units(w, a.ntr, k, ub, ue);
+        float v0 = 0.f, v1 = 0.f;
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            v0[r] = v1[r] = 0.f;
-#pragma unroll
-            for (int ww = 0; ww < G1_NW; ww++) {
-                const float2 p = *reinterpret_cast<const float2*>(red + g1_red_row(k, ww, R, r) + 2 * lane);
-                v0[r] += p.x;
-                v1[r] += p.y;
-            }
+        for (int ww = 0; ww < G1_NW; ww++) {
+            if (!g1_run_meets(g1_wave_run(w.L, ww), ub, ue)) continue;
+            const float2 p = *reinterpret_cast<const float2*>(red + g1_red_row(k, ww, nr, r) + 2 * lane);
+            v0 += p.x;
+            v1 += p.y;
         }
         int g_lo, g_hi;
         g1_contributors<ONE>(a, sht, w.S_first + k, g_lo, g_hi);
         if (g_hi > g_lo) {
-            // split segment: slot (S, g) holds this workgroup's R rows of 128 partials, which
+            // split segment: row r of slot (S, g) holds this workgroup's 128 partials, which
             // gemv1_finish_kernel adds after the launch
             uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + g1_slot(w.S_first + k, g, R)) + lane;
-#pragma unroll
-            for (int r = 0; r < R; r++)
-                my[g1_slot_word(0, R, r)] = (uint64_t)__builtin_bit_cast(uint32_t, v0[r]) |
-                             ((uint64_t)__builtin_bit_cast(uint32_t, v1[r]) << 32);
+            my[g1_slot_word(0, R, r)] = (uint64_t)__builtin_bit_cast(uint32_t, v0) |
+                                        ((uint64_t)__builtin_bit_cast(uint32_t, v1) << 32);
         } else {
-            for (int r = 0; r < nr; r++) finish(k, r, v0[r], v1[r]);
+            finish(k, r, v0, v1);
         }
     }
 }
@@ -339,13 +349,14 @@ __device__ __forceinline__ void g1_finish_body(const G1Group& a, const G1Shard* 
     int g_lo, g_hi;
     g1_contributors<ONE>(a, sht, S, g_lo, g_hi);
     if (g_hi == g_lo) return;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     const int nsl = g_hi - g_lo + 1;
     const int nr = R == 1 ? 1 : a.nrows;
     const uint32_t sv = reinterpret_cast<const uint32_t*>(sh(s).svh + cg * 128)[lane];
     const uint64_t* sl = reinterpret_cast<const uint64_t*>(a.slots + g1_slot(S, g_lo, R)) + lane;
     constexpr int B = 32;
-    for (int r = 0; r < nr; r++) {
+    // wave r of the block finishes activation row r
+    for (int r = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); r < nr; r += R) {
         float v0 = 0.f, v1 = 0.f;
         for (int t0 = 0; t0 < nsl; t0 += B) {
             uint64_t xv[B];
@@ -369,14 +380,14 @@ __device__ __forceinline__ void g1_finish_body(const G1Group& a, const G1Shard* 
 // A single-group launch's split segments (block = segment): every argument field is read at
 // a constant offset, so its scalar loads issue together.
 template <int R, bool ONE>
-__global__ __launch_bounds__(64) void gemv1_finish_kernel(const G1Args a)
+__global__ __launch_bounds__(64 * R) void gemv1_finish_kernel(const G1Args a)
 {
     g1_finish_body<R, ONE>(a.grp, a.sh, blockIdx.x);
 }
 
 // A multi-group launch's split segments: block b is segment b - fbeg[i] of group i.
 template <int R>
-__global__ __launch_bounds__(64) void gemv1_finish_multi_kernel(const G1Multi)
+__global__ __launch_bounds__(64 * R) void gemv1_finish_multi_kernel(const G1Multi)
 {
     const G1Multi& mm = *(const G1Multi*)__builtin_amdgcn_kernarg_segment_ptr();
     const int i = __builtin_amdgcn_readfirstlane(g1_group_of(mm.fbeg, mm.ngrp, (int)blockIdx.x));
@@ -439,7 +450,7 @@ static int g1_launch(const void* fn, void* arg, int G, size_t lds, hipStream_t s
 // Whether 2..4 rows of these shards run well here: every launch keeps at least three
 // workgroups per CU resident (with four rows the LDS per workgroup grows with its range).
 // The caller takes the split kernels otherwise.
-bool gemv1_rows_fit(const GemvShard* shards, int nshards)
+bool gemv1_rows_fit(const GemvShard* shards, int nshards, int rows)
 {
     const int ntr = shards[0].ic / 16;
     const int cus = g1_cu_count();
@@ -455,7 +466,7 @@ bool gemv1_rows_fit(const GemvShard* shards, int nshards)
         }
         if (!ns) continue;
         size_t lds;
-        if (g1_split(U, ns, ntr, G1_ROWS, cus, G, lds) < 3) return false;
+        if (g1_split(U, ns, ntr, rows, cus, G, lds) < 3) return false;
     }
     return true;
 }
@@ -477,7 +488,7 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int 
                                       : (L.one ? reinterpret_cast<const void*>(&gemv1_finish_kernel<G1_ROWS, true>)
                                                : reinterpret_cast<const void*>(&gemv1_finish_kernel<G1_ROWS, false>));
             void* kargs[] = {&args};
-            hipLaunchKernel(ff, dim3(L.fblocks), dim3(64), kargs, 0, stream);
+            hipLaunchKernel(ff, dim3(L.fblocks), dim3(64 * L.R), kargs, 0, stream);
             return check_launch(what);
         }
         G1Multi m = *L.m;
@@ -490,7 +501,7 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int 
         const void* ff = L.R == 1 ? reinterpret_cast<const void*>(&gemv1_finish_multi_kernel<1>)
                                   : reinterpret_cast<const void*>(&gemv1_finish_multi_kernel<G1_ROWS>);
         void* kargs[] = {&m};
-        hipLaunchKernel(ff, dim3(L.fblocks), dim3(64), kargs, 0, stream);
+        hipLaunchKernel(ff, dim3(L.fblocks), dim3(64 * L.R), kargs, 0, stream);
         return check_launch(what);
     });
 }

@@ -22,6 +22,7 @@ constexpr int G1_MAXSH = 8;              // shards per launch
 constexpr int G1_WG_PER_CU = 4;          // target resident workgroups per CU (8 waves / SIMD)
 constexpr int G1_GMAX = 2048;            // workgroups per launch (bounds the slot area)
 constexpr int G1_ROWS = 4;               // activation rows of the multi-row template
+constexpr int G1_TBATCH = 2;             // activation-table pairs a wave loads before transforming
 
 // Units a wave keeps in flight: one.  Eight waves per SIMD already keep enough loads in
 // flight, and every unit more per wave lengthens the memory queues that a launch's first
@@ -293,35 +294,56 @@ G1_HD void g1_contributors(const G1Group& a, const G1Shard* sht, int S, int& g_l
 
 // ---------------------------------------------------------------- LDS layout and indices
 
-// red[nseg][G1_NW][R][128] fp32 partial rows | act[nocc][8][R][16] duplicated fp16
+// Units [b, e) of the range's k-th segment, relative to the range (segments are ntr units;
+// the first one starts at tile row tr0).
+G1_HD void g1_seg_units(const G1Range& w, int ntr, int k, int& b, int& e)
+{
+    const int first = ntr - w.tr0;
+    b = k == 0 ? 0 : first + (k - 1) * ntr;
+    e = first + k * ntr;
+    if (e > w.L) e = w.L;
+}
+
+// Whether a wave's run holds units of [b, e).
+G1_HD bool g1_run_meets(const G1Run& run, int b, int e)
+{
+    return run.n > 0 && run.lo < e && run.lo + run.n > b;
+}
+
+// nr = activation rows the tables hold (1, or the call's rows for the multi-row template).
+// red[nseg + G1_NW - 1][nr][128] fp32 partial rows | act[nocc][8][nr][16] duplicated fp16
 // activations (u32 words) | zero[16] (the A operand of the lanes whose k-block is not theirs).
+// Wave ww's partial rows of the range's k-th segment are red[k + ww]: a wave's run is one
+// contiguous piece of the range and the runs are in wave order, so two (segment, wave) pairs
+// that both hold units never share k + ww (if wave ww meets segment k + 1, wave ww + 1 starts
+// at or after it and cannot meet segment k).  Only such pairs are written and read.
 struct G1Lds {
     int act;                   // u32 offset of act
     int zero;                  // u32 offset of zero
     int words;                 // u32 words in all
 };
 
-G1_HD G1Lds g1_lds_layout(int nseg, int nocc, int R)
+G1_HD G1Lds g1_lds_layout(int nseg, int nocc, int nr)
 {
     G1Lds l;
-    l.act = nseg * G1_NW * R * 128;
-    l.zero = l.act + nocc * R * 128;
+    l.act = (nseg + G1_NW - 1) * nr * 128;
+    l.zero = l.act + nocc * nr * 128;
     l.words = l.zero + 16;
     return l;
 }
 
 // First float of wave ww's partial row r of the range's k-th segment in red.
-G1_HD int g1_red_row(int k, int ww, int R, int r)
+G1_HD int g1_red_row(int k, int ww, int nr, int r)
 {
-    return ((k * G1_NW + ww) * R + r) * 128;
+    return ((k + ww) * nr + r) * 128;
 }
 
 // u32 word (of act) where lane l stores activation row r's outputs 2l, 2l + 1 of occurrence
 // i as two duplicated fp16 pairs: act[i][tile row l / 8][r][m][t] holds row 2m +
 // {0, 1, 8, 9}[t] of the tile row, lane l's rows are m = l % 4, t = 2 ((l % 8) / 4), t + 1.
-G1_HD int g1_act_word(int i, int lane, int R, int r)
+G1_HD int g1_act_word(int i, int lane, int nr, int r)
 {
-    return ((i * 8 + (lane >> 3)) * R + r) * 16 + 4 * (lane & 3) + 2 * ((lane >> 2) & 1);
+    return ((i * 8 + (lane >> 3)) * nr + r) * 16 + 4 * (lane & 3) + 2 * ((lane >> 2) & 1);
 }
 
 // The lane's A operand: row i = lane % 16 in k-block lane / 16, which carries activation row
@@ -332,16 +354,16 @@ G1_HD uint32_t g1_asel(int lane)
     return ((lane & 15) & 3) == (lane >> 4) ? 1u : 0u;
 }
 
-G1_HD uint32_t g1_aoff(int lane, int R, const G1Lds& l)
+G1_HD uint32_t g1_aoff(int lane, int nr, const G1Lds& l)
 {
     const int rr = (lane & 15) >> 2;
-    return g1_asel(lane) ? (uint32_t)(4 * l.act + (rr < R - 1 ? rr : R - 1) * 64) : (uint32_t)(4 * l.zero);
+    return g1_asel(lane) ? (uint32_t)(4 * l.act + (rr < nr - 1 ? rr : nr - 1) * 64) : (uint32_t)(4 * l.zero);
 }
 
 // Byte offset (relative to act) of the table entry of occurrence occ, tile row tr.
-G1_HD uint32_t g1_a_entry(int occ, int tr, int R)
+G1_HD uint32_t g1_a_entry(int occ, int tr, int nr)
 {
-    return (uint32_t)((occ * 8 + (tr & 7)) * R) * 64u;
+    return (uint32_t)((occ * 8 + (tr & 7)) * nr) * 64u;
 }
 
 // Where lane l's accumulators land in a partial row: activation row yrow, outputs
@@ -382,17 +404,18 @@ inline G1Div g1_magic(uint32_t d)
     return G1Div{(uint32_t)(((1ull << (31 + l)) / d) + 1), l - 1};
 }
 
-// Dynamic LDS a launch needs: a partial row per wave for the most segments (shard, column
-// group) a workgroup range of ceil(U / G) units can touch, a transformed activation block for
-// each 128-input block it can meet (at most ceil(L / 8) + nseg + 1: a piece of a segment
-// meets one block more than its length in blocks when it starts inside a block, and only the
-// first piece can), and the 64-byte zero operand.
-inline size_t g1_lds_bytes(int U, int G, int ntr, int R)
+// Dynamic LDS a launch needs for nr activation rows: partial rows for the most segments
+// (shard, column group) a workgroup range of L = ceil(U / G) units can touch (nseg, plus
+// G1_NW - 1: red[k + ww]), a transformed activation block for each 128-input block it can
+// meet, and the 64-byte zero operand.  Segments are ntr units, a multiple of 8, so a
+// range's blocks are the 8-unit-aligned pieces of the unit numbering it meets: at most
+// floor((L + 6) / 8) + 1.
+inline size_t g1_lds_bytes(int U, int G, int ntr, int nr)
 {
     const int L = (U + G - 1) / G;
     const int nseg = (L - 1 + ntr - 1) / ntr + 1;
-    const int nocc = (L + 7) / 8 + nseg + 1;
-    return (size_t)nseg * G1_NW * R * 128 * sizeof(float) + (size_t)nocc * R * 128 * sizeof(uint32_t) + 64;
+    const int nocc = (L + 6) / 8 + 1;
+    return (size_t)(nseg + G1_NW - 1) * nr * 128 * sizeof(float) + (size_t)nocc * nr * 128 * sizeof(uint32_t) + 64;
 }
 
 // Row-count template of a call: one activation row, or up to four (G1_ROWS).
@@ -471,14 +494,15 @@ inline bool g1_any_split(const G1Group& grp)
 
 constexpr size_t G1_LDS_PER_CU = 160 * 1024;
 
-// Workgroup counts G[0..ns) of one launch whose groups have U[t] units, for the most
+// Workgroup counts G[0..ns) of one launch whose groups have U[t] units (nr activation rows in
+// the tables), for the most
 // workgroups per CU (up to G1_WG_PER_CU) whose LDS lets them all stay resident; returns
 // that number and the launch's LDS per workgroup.  When even one workgroup per CU cannot hold
 // its range (few CUs, or a very large shard), the launch takes more workgroups than stay
 // resident -- G1_UNITS_PER_WG units each, up to G1_GMAX; no workgroup waits for another, so
 // they simply run in turn -- and 0 is returned.  The caller refuses a launch whose LDS still
 // exceeds G1_LDS_PER_CU.
-inline int g1_split(const long* U, int ns, int ntr, int R, int cus, int* G, size_t& lds)
+inline int g1_split(const long* U, int ns, int ntr, int nr, int cus, int* G, size_t& lds)
 {
     auto share = [&](int gmax) {
         long Gsum = 0;
@@ -489,7 +513,7 @@ inline int g1_split(const long* U, int ns, int ntr, int R, int cus, int* G, size
         if (Gsum > gmax)   // share the workgroups in proportion to the groups' sizes
             for (int t = 0; t < ns; t++) G[t] = std::max(1, (int)((long)G[t] * gmax / Gsum));
         lds = 0;
-        for (int t = 0; t < ns; t++) lds = std::max(lds, g1_lds_bytes((int)U[t], G[t], ntr, R));
+        for (int t = 0; t < ns; t++) lds = std::max(lds, g1_lds_bytes((int)U[t], G[t], ntr, nr));
     };
     for (int wgpc = G1_WG_PER_CU; wgpc >= 1; wgpc--) {
         share(std::min(G1_GMAX, wgpc * cus));
@@ -566,7 +590,7 @@ int g1_plan(const uint16_t* A, const GemvShard* shards, int nshards, int rows, c
         G1Launch L = {};
         L.cb = gcb[j0];
         L.R = R;
-        g1_split(U, ns, ntr, R, cus, G, L.lds);
+        g1_split(U, ns, ntr, R == 1 ? 1 : rows, cus, G, L.lds);
         if (L.lds > G1_LDS_PER_CU)
             return set_error(EXL3_ERR_ARG,
                              "exl3_gemv: %ld tile-row units need %zu bytes of LDS per workgroup (limit %zu)",

@@ -116,7 +116,8 @@ void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G
     const G1Range w = g1_range<ONE>(a, sht, g);
     if (w.L < 1) fail("launch %d wg %d: empty range", launch, g);
     if (w.nseg < 1 || w.nocc < 1) fail("launch %d wg %d: nseg %d nocc %d", launch, g, w.nseg, w.nocc);
-    const G1Lds ll = g1_lds_layout(w.nseg, w.nocc, R);
+    const int nr = R == 1 ? 1 : a.nrows;
+    const G1Lds ll = g1_lds_layout(w.nseg, w.nocc, nr);
     if ((size_t)ll.words * 4 > lds)
         fail("launch %d wg %d: LDS layout %d bytes > launch LDS %zu", launch, g, ll.words * 4, lds);
     const int ntr = a.ntr;
@@ -128,45 +129,44 @@ void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G
     };
     auto trellis_words = [&](int gi) { return (long)(W.sh[gi].ic / 16) * (W.sh[gi].oc / 16) * 8 * K; };
 
-    // ---- zero operand and partial rows
+    // ---- zero operand
     for (int t = 0; t < 16; t++)
         if (ll.zero + t >= ll.words) fail("zero word out of LDS");
-    for (int k = 0; k < w.nseg; k++)
-        for (int wave = 0; wave < G1_NW; wave++)
-            for (int r = 0; r < R; r++)
-                for (int lane = 0; lane < 64; lane++) {
-                    const int i0 = g1_red_row(k, wave, R, r) + 2 * lane;
-                    if (i0 < 0 || i0 + 2 > ll.act) fail("red zeroing outside red");
-                }
 
-    // ---- activation table: tag of each occurrence (segment k, block) and rows written
-    std::vector<int> occ_k(w.nocc, -1), occ_blk(w.nocc, -1);
+    // ---- activation table: tag of each occurrence (segment k, block); each (occurrence, row)
+    // transformed once
+    std::vector<int> occ_k(w.nocc, -1), occ_blk(w.nocc, -1), occ_rows(w.nocc, 0);
     for (int wave = 0; wave < G1_NW; wave++)
-        for (int i = wave; i < w.nocc; i += G1_NW) {
+        for (int t = wave; t < w.nocc * nr; t += G1_NW) {
+            const int i = R == 1 ? t : t / nr, r = t - i * nr;
             int k, blk;
             g1_occ_block(a, w, i, k, blk);
             if (k < 0 || k >= w.nseg) fail("occurrence %d: segment %d of %d", i, k, w.nseg);
             if (blk < 0 || blk >= ntr / 8) fail("occurrence %d: block %d of %d", i, blk, ntr / 8);
-            if (occ_k[i] >= 0) fail("occurrence %d written twice", i);
+            if (occ_k[i] >= 0 && (occ_k[i] != k || occ_blk[i] != blk)) fail("occurrence %d: two blocks", i);
             occ_k[i] = k;
             occ_blk[i] = blk;
+            if (occ_rows[i] & (1 << r)) fail("occurrence %d row %d transformed twice", i, r);
+            occ_rows[i] |= 1 << r;
             const int s = g1_shard_of_seg<ONE>(a, sht, w.S_first + k);
             const int gi = shard_of(s);
             const G1Shard& e = g1_sh<ONE>(sht, s);
             for (int lane = 0; lane < 64; lane++) {
                 need_in(reinterpret_cast<const uint32_t*>(e.suh + blk * 128) + lane, 4, B_SUH + gi,
                         (long)W.sh[gi].ic * 2, "suh load");
-                for (int r = 0; r < R; r++) {
-                    need_in(reinterpret_cast<const uint32_t*>(a.x + g1_x_elem(a, r, blk)) + lane, 4, B_X,
-                            (long)W.rows * ic * 2, "activation load");
-                    const int aw = g1_act_word(i, lane, R, r);
-                    if (aw < 0 || aw + 2 > ll.zero - ll.act) fail("act store outside act (word %d)", aw);
-                }
+                need_in(reinterpret_cast<const uint32_t*>(a.x + g1_x_elem(a, r, blk)) + lane, 4, B_X,
+                        (long)W.rows * ic * 2, "activation load");
+                if (g1_x_elem(a, r, blk) / ic != r) fail("activation row %d reads row %ld", r, g1_x_elem(a, r, blk) / ic);
+                const int aw = g1_act_word(i, lane, nr, r);
+                if (aw < 0 || aw + 2 > ll.zero - ll.act) fail("act store outside act (word %d)", aw);
             }
         }
+    for (int i = 0; i < w.nocc; i++)
+        if (occ_rows[i] != (1 << nr) - 1) fail("occurrence %d: rows %x transformed, %d needed", i, occ_rows[i], nr);
 
     // ---- per wave: prefetch and processing cursors, LDS reads, flushes
     std::vector<int> red_written((size_t)w.nseg * G1_NW, 0);
+    std::vector<int> red_slot((size_t)w.nseg + G1_NW, -1);   // which (segment, wave) holds red[k + ww]
     for (int wave = 0; wave < G1_NW; wave++) {
         const G1Run run = g1_wave_run(w.L, wave);
         const int n = run.n;
@@ -198,12 +198,14 @@ void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G
             if (cur < 0 || cur >= w.nseg) fail("flush of segment %d of %d", cur, w.nseg);
             for (int lane = 0; lane < 64; lane++) {
                 const int yrow = g1_yrow(lane), ycol = g1_ycol(lane);
-                if (yrow >= R) continue;
-                const int base = g1_red_row(cur, wave, R, yrow) + ycol;
+                if (yrow >= nr) continue;
+                const int base = g1_red_row(cur, wave, nr, yrow) + ycol;
                 for (int e = 0; e < 4; e++)
                     if (base + 32 * e + 8 >= ll.act || base + 32 * e < 0) fail("flush outside red");
             }
-            red_written[(size_t)cur * G1_NW + wave]++;
+            if (red_written[(size_t)cur * G1_NW + wave]++) fail("wave %d flushes segment %d twice", wave, cur);
+            if (red_slot[cur + wave] >= 0) fail("partial rows (%d, %d) and %d share red[%d]", cur, wave, red_slot[cur + wave], cur + wave);
+            red_slot[cur + wave] = cur * G1_NW + wave;
             cur = k;
         };
         for (int j = 0; j < n; j += D)
@@ -221,16 +223,16 @@ void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G
                     if (occ_k[occ] != cur || occ_blk[occ] != (cu.tr >> 3))
                         fail("unit (seg %d, tr %d) reads occurrence %d = (seg %d, block %d)", cur, cu.tr, occ,
                              occ_k[occ], occ_blk[occ]);
-                    const uint32_t ent = g1_a_entry(occ, cu.tr, R);
+                    const uint32_t ent = g1_a_entry(occ, cu.tr, nr);
                     for (int lane = 0; lane < 64; lane++) {
-                        const uint32_t asel = g1_asel(lane), aoff = g1_aoff(lane, R, ll);
+                        const uint32_t asel = g1_asel(lane), aoff = g1_aoff(lane, nr, ll);
                         const uint32_t byte = ent * asel + aoff;
                         if (asel) {
                             if (byte < 4u * ll.act || byte + 64 > 4u * ll.zero) fail("A read outside act");
                             // it must be the table row (occurrence, tile row, activation row)
                             const uint32_t rel = (byte - 4u * ll.act) / 64;
-                            const int want_r = std::min((lane & 15) >> 2, R - 1);
-                            if (rel != (uint32_t)((occ * 8 + (cu.tr & 7)) * R + want_r)) fail("A read of a wrong table row");
+                            const int want_r = std::min((lane & 15) >> 2, nr - 1);
+                            if (rel != (uint32_t)((occ * 8 + (cu.tr & 7)) * nr + want_r)) fail("A read of a wrong table row");
                         } else if (byte != 4u * ll.zero) {
                             fail("zero-operand lane reads byte %u, not the zero words", byte);
                         }
@@ -249,12 +251,20 @@ void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G
     }
 
     // ---- tail: per segment, finish here or store the slot
-    const int nr = R == 1 ? 1 : a.nrows;
     for (int wave = 0; wave < G1_NW; wave++)
         for (int k = wave; k < w.nseg; k += G1_NW) {
-            for (int r = 0; r < R; r++)
-                for (int ww = 0; ww < G1_NW; ww++)
-                    if (g1_red_row(k, ww, R, r) + 128 > ll.act) fail("red read outside red");
+            // the tail sums the rows of the waves whose runs meet segment k: each must have been
+            // flushed, and every flushed row of segment k must be among them
+            int ub, ue;
+            g1_seg_units(w, a.ntr, k, ub, ue);
+            for (int ww = 0; ww < G1_NW; ww++) {
+                const bool meets = g1_run_meets(g1_wave_run(w.L, ww), ub, ue);
+                if (meets != (red_written[(size_t)k * G1_NW + ww] == 1))
+                    fail("segment %d: wave %d meets %d but flushed %d times", k, ww, meets, red_written[(size_t)k * G1_NW + ww]);
+                if (!meets) continue;
+                for (int r = 0; r < nr; r++)
+                    if (g1_red_row(k, ww, nr, r) + 128 > ll.act) fail("red read outside red");
+            }
             const int S = w.S_first + k;
             int g_lo, g_hi;
             g1_contributors<ONE>(a, sht, S, g_lo, g_hi);
@@ -266,7 +276,7 @@ void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G
             if (cg < 0 || cg >= e.ncg) fail("segment %d: column group %d of %d", S, cg, e.ncg);
             if (g_hi > g_lo) {
                 const float* base = a.slots + g1_slot(S, g, R);
-                for (int r = 0; r < R; r++) {
+                for (int r = 0; r < nr; r++) {
                     const uint64_t* row = reinterpret_cast<const uint64_t*>(base) + g1_slot_word(0, R, r);
                     need_in(row, 64 * 8, B_SLOTS, (long)W.slot_bytes, "slot store");
                     need_in(row, 64 * 8, B_SLOTS, off_of(a.slots) + (long)(a.G + a.nsegs) * R * 128 * 4,

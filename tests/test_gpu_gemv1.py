@@ -94,3 +94,22 @@ def test_gemv1_lm_head_sampled_column_groups(native, oracle):
         sl = slice(cg * 128, (cg + 1) * 128)
         lin = dict(trellis=t[:, cg * 8:(cg + 1) * 8].contiguous(), suh=suh, svh=svh[sl].contiguous(), K=K)
         check(y[:, sl], x, lin, 0, oracle)
+
+
+@pytest.mark.parametrize("rows", [2, 4])
+def test_gemv_split_kernels_on_a_wide_shard(native, oracle, rows):
+    """2..4 rows of the lm_head shape (5120 -> 151936, K=6): with four activation rows its
+    workgroup ranges would need more LDS than three resident workgroups per CU leave, so the
+    call takes the split kernels (gemv_partial_kernel + gemv_reduce_kernel); four column
+    groups are checked against the oracle on the matching trellis slice."""
+    ic, oc, K = 5120, 151936, 6
+    g = torch.Generator().manual_seed(5)
+    t = syn.trellis(ic, oc, K, g)
+    suh = syn.signs(ic, g)
+    svh = syn.svh(ic, oc, g)
+    x = syn.activations(rows, ic, torch.Generator().manual_seed(42 + rows))
+    y = native.gemv(x.to(dev()), t.to(dev()), suh.to(dev()), svh.to(dev()), K, 0).cpu()
+    for cg in (0, 7, 600, 1186):
+        sl = slice(cg * 128, (cg + 1) * 128)
+        lin = dict(trellis=t[:, cg * 8:(cg + 1) * 8].contiguous(), suh=suh, svh=svh[sl].contiguous(), K=K)
+        check(y[:, sl], x, lin, 0, oracle)
