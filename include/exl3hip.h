@@ -93,7 +93,8 @@ int exl3_had_r_128(const void* in, void* out, const void* pre, const void* post,
  * [orcasaq2/ops.py:46-49] for rows <= 16 (the A_had scratch is internal to the kernel).
  * rows 1..4 take one decode launch per codebook (followed, when a column group's inputs
  * were split over several workgroups, by one small kernel that adds the split partial
- * sums); 5..16 rows take a set-up kernel and one launch per codebook.
+ * sums); 5..16 rows take a set-up kernel (every shard's transformed activations), then per
+ * codebook one decode launch and one finishing launch.
  */
 size_t exl3_gemv_workspace_bytes(int rows, int ic, int oc);
 int exl3_gemv(const void* A, const void* trellis, void* C, const void* suh, const void* svh,
@@ -131,7 +132,7 @@ int exl3_gemv_grouped(const void* A, const exl3_shard_t* shards, int nshards, vo
  * The scratch is a file-scope device array of EXL3_STATIC_SCRATCH_BYTES (16 MiB), one per
  * GPU, held until the process ends; a call whose exl3_gemv_grouped_workspace_bytes exceeds
  * it fails with EXL3_ERR_WORKSPACE (rows 1..4 fit every shape of the 27B model and its
- * 151936-wide lm_head; rows 5..16 fit single 5120-output shards).  All calls on one GPU
+ * 151936-wide lm_head; rows 5..16 fit every layer of that model and its lm_head).  All calls on one GPU
  * share the array and each leaves it ready for the next, so calls issued in order (one
  * stream, or graph replays in order) are safe; calls that may overlap in time race on it.
  */

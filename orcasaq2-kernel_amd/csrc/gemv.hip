@@ -6,8 +6,8 @@
 //   * 1: gemv1.hip (persistent decode, MFMA multiply-accumulate);
 //   * 2..GV_SPLIT_MAX_ROWS: gemv1.hip as well where its launch keeps three workgroups per
 //     CU resident (gemv1_rows_fit), else the two kernels below;
-//   * above: gemm_sk.hip with 16-row tiles (decode into LDS once per tile, MFMA from LDS;
-//     the cost hardly depends on the row count).
+//   * above (5..16): gemv16.hip (the batch-1 decode on 4 x 2-tile units, one MFMA serving all
+//     16 rows; the cost hardly depends on the row count).
 //
 // Two kernels, no inter-workgroup synchronisation inside a kernel (an agent-scope fence
 // on this part writes back and invalidates the whole per-XCD L2, which serialises):
@@ -78,7 +78,7 @@ size_t gemv_workspace_bytes(int rows, int ic, int oc)
     if (rows <= GV_SPLIT_MAX_ROWS)   // either path: the 1..4-row kernel's slots or the split partials
         return align256(std::max(gemv1_slot_bytes(ic, oc, rows),
                                  (size_t)gemv_splits(ic, oc) * rows * oc * sizeof(float)));
-    if (rows > GV_SPLIT_MAX_ROWS) return align256(gemv_sk_bytes(rows, ic, oc));
+    if (rows > GV_SPLIT_MAX_ROWS) return align256(gemv16_shard_bytes(ic, oc));
     return align256((size_t)gemv_splits(ic, oc) * rows * oc * sizeof(float));
 }
 
@@ -308,8 +308,8 @@ int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int r
         return gemv1_dispatch(A, shards, nshards, rows, ws + GEMV_COUNTER_BYTES, offs[nshards] - GEMV_COUNTER_BYTES,
                               stream);
     if (rows > GV_SPLIT_MAX_ROWS)
-        return gemv_sk_dispatch(A, shards, nshards, rows, ws + GEMV_COUNTER_BYTES, offs[nshards] - GEMV_COUNTER_BYTES,
-                                stream);
+        return gemv16_dispatch(A, shards, nshards, rows, ws + GEMV_COUNTER_BYTES, offs[nshards] - GEMV_COUNTER_BYTES,
+                               stream);
     bool done[EXL3_MAX_SHARDS] = {false};
     const size_t lds = hx_bytes(rows);
     for (int i = 0; i < nshards; i++) {

@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "../gemm_sk_plan.h"
+#include "../gemv16_plan.h"
 #include "../gemv1_plan.h"
 
 namespace exl3 {
@@ -738,6 +739,203 @@ void sk_replay_any(SkWorld& W, const GemvShard* shards, const SkLaunch& L, int l
     if (L.K == 0 && !sk_has_k0<256>() && L.BM == 256) fail("per-shard-K launch of 256-row tiles");
 }
 
+
+// ================================================================ gemv16 (5..16 rows)
+
+struct G16World {
+    int rows, ic;
+    std::vector<ShardSpec> sh;
+    std::vector<int> col0;
+    long ldc;
+    size_t ws_bytes;
+    std::vector<uint8_t> out;
+    std::vector<long> unit_base;
+    std::vector<uint8_t> unit_seen;
+    std::vector<std::vector<uint8_t>> ah_written;   // per shard, per fragment word
+    std::vector<long> ah_off;                       // workspace byte offset of each shard's fragments
+    std::map<long, std::tuple<int, int, int>> slots;   // float offset -> (launch, strip, workgroup)
+    std::map<long, int> slot_reads;
+    long loads = 0;
+};
+
+int g16_shard_index(const G16World& W, const GemvShard* shards, const uint32_t* trellis)
+{
+    for (size_t i = 0; i < W.sh.size(); i++)
+        if (shards[i].trellis == trellis) return (int)i;
+    return -1;
+}
+
+void g16_replay_prep(G16World& W, const G16Prep& p)
+{
+    const long waves = 4 * (((long)p.nsh * p.rows * p.nblk + 3) / 4);
+    for (long w = 0; w < waves; w++) {
+        if (w >= (long)p.nsh * p.rows * p.nblk) continue;
+        int s, r, b;
+        g16_prep_wave(p, (int)w, s, r, b);
+        if (s >= p.nsh || r >= p.rows || b >= p.nblk) fail("set-up wave %ld -> (%d, %d, %d)", w, s, r, b);
+        const long words = g16_ah_words(p.ic);
+        if (buf_of(p.ah[s]) != B_WS || off_of(p.ah[s]) != W.ah_off[s]) fail("fragments of shard %d misplaced", s);
+        if (W.ah_off[s] + words * 4 > (long)W.ws_bytes) fail("fragments of shard %d beyond the workspace", s);
+        for (int lane = 0; lane < 64; lane++) {
+            need_in(reinterpret_cast<const uint32_t*>(p.A + (long)r * p.ic + b * 128) + lane, 4, B_X, (long)W.rows * W.ic * 2, "A load (set-up)");
+            need_in(reinterpret_cast<const uint32_t*>(p.suh[s] + b * 128) + lane, 4, B_SUH + s, (long)W.ic * 2, "suh load (set-up)");
+            const long e = g16_ah_elem(r, b * 128 + 2 * lane);
+            if (e < 0 || e + 2 > words || (e & 1)) fail("fragment store %ld of %ld", e, words);
+            for (int t = 0; t < 2; t++) {
+                if (W.ah_written[s][e + t]) fail("fragment word %ld of shard %d written twice", e + t, s);
+                W.ah_written[s][e + t] = 1;
+            }
+        }
+    }
+}
+
+template <int K, bool ONE>
+void g16_replay_wg(G16World& W, const GemvShard* shards, const G1Group& a, const G16Shard* sht, int g, size_t lds,
+                   int launch)
+{
+    const G1Range w = g16_range<ONE>(a, sht, g);
+    if (w.L < 1 || w.nseg < 1) fail("gemv16 wg %d: L %d nseg %d", g, w.L, w.nseg);
+    const int red_floats = g16_red_bytes(w.nseg) / 4;
+    if ((size_t)red_floats * 4 > lds) fail("gemv16 wg %d: %d bytes of partial rows > launch LDS %zu", g, red_floats * 4, lds);
+    const int nq = a.ntr;
+    auto shard_of = [&](int s) {
+        if (s < 0 || s >= a.nshards) fail("gemv16: shard %d of %d", s, a.nshards);
+        return g16_shard_index(W, shards, g16_sh<ONE>(sht, s).trellis);
+    };
+    std::vector<int> flushed((size_t)w.nseg * G1_NW, 0), red_slot((size_t)w.nseg + G1_NW, -1);
+    for (int wave = 0; wave < G1_NW; wave++) {
+        const G1Run run = g1_wave_run(w.L, wave);
+        const int n = run.n;
+        G16Cursor pf = g16_cursor_at<K, ONE>(a, sht, w.ub + run.lo), cu = pf;
+        int jpf = 0;
+        auto check_load = [&](const G16Cursor& c) {
+            const int gi = shard_of(c.s);
+            const G16Shard& e = g16_sh<ONE>(sht, c.s);
+            if (c.strip < 0 || c.strip >= e.nstrip || c.q < 0 || c.q >= nq) fail("gemv16 cursor strip %d q %d", c.strip, c.q);
+            const long tw = (long)(W.sh[gi].ic / 16) * (W.sh[gi].oc / 16) * 8 * K;
+            for (int lane = 0; lane < 64; lane++) {
+                const uint32_t* p = c.p + g16_lane_word(lane, e.oc16, K);
+                need_in(p, 4L * K, B_TRELLIS + gi, tw * 4, "gemv16 trellis load");
+                const long wd = off_of(p) / 4, tile = wd / (8 * K), ti = tile / e.oc16, tj = tile % e.oc16;
+                if (ti != 4 * c.q + (lane >> 4) || tj != 2 * c.strip + ((lane & 15) >> 3) || (wd % (8 * K)) != (lane & 7) * K)
+                    fail("gemv16 lane %d loads tile (%ld, %ld) word %ld", lane, ti, tj, wd % (8 * K));
+                for (int m = 0; m < 4; m++) {
+                    const uint32_t* ap = c.ah + g16_ah_word(m, lane);
+                    need_in(ap, 16, B_WS, W.ah_off[gi] + g16_ah_words(W.ic) * 4, "gemv16 fragment load");
+                    const long rel = (off_of(ap) - W.ah_off[gi]) / 4;
+                    if (rel < 0) fail("gemv16 fragment load before the shard's fragments");
+                    // the four words are row i's inputs 64 q + 16 j + 2 m + {0, 1, 8, 9}
+                    const int i = lane & 15, j = lane >> 4;
+                    const int o[4] = {0, 1, 8, 9};
+                    for (int t = 0; t < 4; t++) {
+                        if (g16_ah_elem(i, 64 * c.q + 16 * j + 2 * m + o[t]) != rel + t) fail("gemv16 fragment word of the wrong input");
+                        if (i < a.nrows && !W.ah_written[gi][rel + t]) fail("gemv16 reads a fragment word the set-up did not write");
+                    }
+                }
+            }
+            W.loads++;
+        };
+        if (n > 0) check_load(pf);
+        int cur = cu.S - w.S_first;
+        auto flush = [&](int k) {
+            if (cur < 0 || cur >= w.nseg) fail("gemv16 flush of strip %d of %d", cur, w.nseg);
+            for (int lane = 0; lane < 64; lane++)
+                for (int h = 0; h < 2; h++)
+                    for (int t = 0; t < 4; t++) {
+                        const int i = g16_red_row(cur, wave) + g16_acc_index(lane, h, t);
+                        if (i < 0 || i >= red_floats) fail("gemv16 flush outside red");
+                    }
+            if (flushed[(size_t)cur * G1_NW + wave]++) fail("gemv16 wave %d flushes strip %d twice", wave, cur);
+            if (red_slot[cur + wave] >= 0) fail("gemv16 partial rows share red[%d]", cur + wave);
+            red_slot[cur + wave] = cur;
+            cur = k;
+        };
+        for (int j = 0; j < n; j++) {
+            if (cu.S - w.S_first != cur) flush(cu.S - w.S_first);
+            const int gi = shard_of(cu.s);
+            const G16Shard& e = g16_sh<ONE>(sht, cu.s);
+            if (cu.S != e.sbeg + cu.strip) fail("gemv16 cursor strip bookkeeping");
+            const long uid = W.unit_base[gi] + (long)cu.strip * nq + cu.q;
+            if (W.unit_seen[uid]++) fail("gemv16 unit (shard %d, strip %d, q %d) twice", gi, cu.strip, cu.q);
+            if (j + 1 < n) g16_advance<K, ONE>(a, sht, cu);
+            g16_next_pf<K, ONE>(a, sht, pf, jpf, n);
+            check_load(pf);
+        }
+        if (n > 0) flush(cur);
+    }
+    // tail: per strip into this workgroup's slot
+    for (int k = 0; k < w.nseg; k++) {
+        int ub, ue;
+        g1_seg_units(w, nq, k, ub, ue);
+        for (int ww = 0; ww < G1_NW; ww++) {
+            const bool meets = g1_run_meets(g1_wave_run(w.L, ww), ub, ue);
+            if (meets != (flushed[(size_t)k * G1_NW + ww] == 1)) fail("gemv16 strip %d wave %d meets %d flushed %d", k, ww, meets, flushed[(size_t)k * G1_NW + ww]);
+            if (meets && g16_red_row(k, ww) + 512 > red_floats) fail("gemv16 red read outside red");
+        }
+        int g_lo, g_hi;
+        g16_contributors<ONE>(a, sht, w.S_first + k, g_lo, g_hi);
+        if (g < g_lo || g > g_hi) fail("gemv16 wg %d holds strip %d, contributors %d..%d", g, w.S_first + k, g_lo, g_hi);
+        const float* sl = a.slots + g16_slot(w.S_first + k, g);
+        need_in(sl, 16 * 32 * 4, B_WS, (long)W.ws_bytes, "gemv16 slot store");
+        need_in(sl, 16 * 32 * 4, B_WS, off_of(a.slots) + (long)(a.G + a.nsegs) * 16 * 32 * 4, "gemv16 slot store (group share)");
+        if (W.slots.count(off_of(sl))) fail("gemv16 slot of strip %d wg %d written twice", w.S_first + k, g);
+        W.slots[off_of(sl)] = std::make_tuple(launch, w.S_first + k, g);
+    }
+}
+
+template <bool ONE>
+void g16_replay_wg_k(int K, G16World& W, const GemvShard* shards, const G1Group& a, const G16Shard* sht, int g,
+                     size_t lds, int launch)
+{
+    switch (K) {
+    case 1: g16_replay_wg<1, ONE>(W, shards, a, sht, g, lds, launch); break;
+    case 2: g16_replay_wg<2, ONE>(W, shards, a, sht, g, lds, launch); break;
+    case 3: g16_replay_wg<3, ONE>(W, shards, a, sht, g, lds, launch); break;
+    case 4: g16_replay_wg<4, ONE>(W, shards, a, sht, g, lds, launch); break;
+    case 5: g16_replay_wg<5, ONE>(W, shards, a, sht, g, lds, launch); break;
+    case 6: g16_replay_wg<6, ONE>(W, shards, a, sht, g, lds, launch); break;
+    case 7: g16_replay_wg<7, ONE>(W, shards, a, sht, g, lds, launch); break;
+    case 8: g16_replay_wg<8, ONE>(W, shards, a, sht, g, lds, launch); break;
+    default: fail("K=%d", K);
+    }
+}
+
+template <bool ONE>
+void g16_replay_finish(G16World& W, const GemvShard* shards, const G1Group& a, const G16Shard* sht, int cg4, int launch)
+{
+    if (cg4 * 4 >= a.nsegs) return;
+    const int s = g16_shard_of_seg<ONE>(a, sht, 4 * cg4);
+    const G16Shard& e = g16_sh<ONE>(sht, s);
+    const int gi = g16_shard_index(W, shards, e.trellis);
+    const int cg = cg4 - e.sbeg / 4;
+    if (e.sbeg % 4 || cg < 0 || cg * 4 >= e.nstrip) fail("gemv16 finish: column group %d", cg);
+    for (int lane = 0; lane < 64; lane++) {
+        const int S = 4 * cg4 + (lane >> 4);
+        if (g16_shard_of_seg<ONE>(a, sht, S) != s) fail("gemv16 finish: strips of one block in two shards");
+        int g_lo, g_hi;
+        g16_contributors<ONE>(a, sht, S, g_lo, g_hi);
+        const int col = (2 * lane) & 31;
+        for (int r = 0; r < a.nrows; r++) {
+            for (int gg = g_lo; gg <= g_hi; gg++) {
+                const float* p = a.slots + g16_slot(S, gg) + r * G16_STRIP + col;
+                need_in(p, 8, B_WS, (long)W.ws_bytes, "gemv16 slot load");
+                const long base = off_of(a.slots + g16_slot(S, gg));
+                auto it = W.slots.find(base);
+                if (it == W.slots.end() || it->second != std::make_tuple(launch, S, gg)) fail("gemv16 finish reads a slot not written for (strip %d, wg %d)", S, gg);
+                W.slot_reads[base]++;
+            }
+            need_in(reinterpret_cast<const uint32_t*>(e.svh + cg * 128) + lane, 4, B_SVH + gi, (long)W.sh[gi].oc * 2, "gemv16 svh load");
+            const uint16_t* o = e.C + r * e.ldc + cg * 128 + 2 * lane;
+            need_in(o, 4, B_C, (long)W.rows * W.ldc * 2, "gemv16 output store");
+            const long el = off_of(o) / 2;
+            const long c = el % W.ldc;
+            if (el / W.ldc != r || c < W.col0[gi] || c + 2 > W.col0[gi] + W.sh[gi].oc) fail("gemv16 output outside shard");
+            W.out[el]++;
+            W.out[el + 1]++;
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -869,6 +1067,107 @@ int exl3r_gemm_sk(int mode, int rows, int ic, int nshards, const int* oc, const 
             stats[1] = W.loads;
             stats[2] = W.pieces;
             stats[3] = W.slot_writes;
+        }
+        return 0;
+    } catch (const Fail& f) {
+        g_msg = f.what;
+        return g_msg.rfind("plan refused", 0) == 0 ? 2 : 1;
+    }
+}
+
+
+// The 5..16-row GEMV (exl3_gemv with 5..16 rows): the set-up kernel, each decode launch and its
+// finish launch, as exl3r_gemv1.  stats: launches, unit loads checked, 0, slots written.
+int exl3r_gemv16(int rows, int ic, int nshards, const int* oc, const int* K, const int* cb, int cus, long long* stats)
+{
+    g_msg.clear();
+    try {
+        if (nshards < 1 || nshards > EXL3_MAX_SHARDS) fail("nshards %d", nshards);
+        G16World W;
+        W.rows = rows;
+        W.ic = ic;
+        std::vector<GemvShard> shards(nshards);
+        long cols = 0, ub = 0;
+        size_t ws = 0;
+        for (int i = 0; i < nshards; i++) {
+            W.sh.push_back(ShardSpec{ic, oc[i], K[i], cb[i]});
+            W.col0.push_back((int)cols);
+            cols += oc[i];
+            ws += (g16_shard_bytes(ic, oc[i]) + 255) & ~(size_t)255;
+            W.unit_base.push_back(ub);
+            ub += (long)(oc[i] / G16_STRIP) * (ic / G16_QIN);
+            W.ah_written.emplace_back(g16_ah_words(ic), 0);
+            W.ah_off.push_back((long)i * (((size_t)g16_ah_words(ic) * 4 + 255) & ~(size_t)255));
+        }
+        W.ldc = cols;
+        W.ws_bytes = ws;
+        W.out.assign((size_t)rows * cols + 2, 0);
+        W.unit_seen.assign(ub, 0);
+        for (int i = 0; i < nshards; i++) {
+            GemvShard& d = shards[i];
+            d.trellis = fake_ptr<uint32_t>(B_TRELLIS + i);
+            d.suh = fake_ptr<uint16_t>(B_SUH + i);
+            d.svh = fake_ptr<uint16_t>(B_SVH + i);
+            d.C = fake_ptr<uint16_t>(B_C) + W.col0[i];
+            d.ic = ic;
+            d.oc = oc[i];
+            d.K = K[i];
+            d.cb = cb[i];
+            d.ldc = W.ldc;
+        }
+        int launch = 0;
+        bool prepped = false;
+        G16Prep prep;
+        const int rc = g16_plan(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, cus, prep,
+                                [&](const G16Launch& L) {
+            if (!prepped) {
+                g16_replay_prep(W, prep);
+                prepped = true;
+            }
+            if (L.lds > G1_LDS_PER_CU) fail("gemv16 launch %d: %zu bytes of LDS", launch, L.lds);
+            if (!L.multi) {
+                const G1Group& a = L.args->grp;
+                for (int g = 0; g < L.G; g++) {
+                    if (L.one) g16_replay_wg_k<true>(L.K, W, shards.data(), a, L.args->sh, g, L.lds, launch);
+                    else g16_replay_wg_k<false>(L.K, W, shards.data(), a, L.args->sh, g, L.lds, launch);
+                }
+                if (L.fblocks * 4 != a.nsegs) fail("gemv16 finish blocks %d for %d strips", L.fblocks, a.nsegs);
+                for (int b = 0; b < L.fblocks; b++) {
+                    if (L.one) g16_replay_finish<true>(W, shards.data(), a, L.args->sh, b, launch);
+                    else g16_replay_finish<false>(W, shards.data(), a, L.args->sh, b, launch);
+                }
+            } else {
+                const G16Multi& m = *L.m;
+                for (int b = 0; b < L.G; b++) {
+                    const int i = g1_group_of(m.gbeg, m.ngrp, b);
+                    const int g = b - m.gbeg[i];
+                    if (g < 0 || g >= m.grp[i].G) fail("gemv16 multi: block %d -> group %d wg %d", b, i, g);
+                    g16_replay_wg_k<false>(m.K[i], W, shards.data(), m.grp[i], m.sh + m.sh0[i], g, L.lds, launch);
+                }
+                for (int b = 0; b < L.fblocks; b++) {
+                    const int i = g1_group_of(m.fbeg, m.ngrp, b);
+                    g16_replay_finish<false>(W, shards.data(), m.grp[i], m.sh + m.sh0[i], b - m.fbeg[i], launch);
+                }
+            }
+            launch++;
+            return EXL3_OK;
+        });
+        if (rc != EXL3_OK) fail("plan refused: %s", exl3::g_err);
+        for (size_t u = 0; u < W.unit_seen.size(); u++)
+            if (W.unit_seen[u] != 1) fail("gemv16 unit %zu decoded %d times", u, W.unit_seen[u]);
+        for (auto& kv : W.slots)
+            if (W.slot_reads[kv.first] < 1) fail("gemv16 slot of strip %d wg %d never read", std::get<1>(kv.second), std::get<2>(kv.second));
+        for (int r = 0; r < rows; r++)
+            for (int i = 0; i < nshards; i++)
+                for (int c = 0; c < oc[i]; c++) {
+                    const uint8_t n = W.out[(size_t)r * W.ldc + W.col0[i] + c];
+                    if (n != 1) fail("gemv16 output row %d shard %d column %d written %d times", r, i, c, n);
+                }
+        if (stats) {
+            stats[0] = launch;
+            stats[1] = W.loads;
+            stats[2] = 0;
+            stats[3] = (long long)W.slots.size();
         }
         return 0;
     } catch (const Fail& f) {

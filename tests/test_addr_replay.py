@@ -138,6 +138,47 @@ def test_gemv1_random_shapes(rl):
         ok(gemv1(rl, rows, ic, ocs, Ks, cbs, cus), f"case {case}: rows={rows} ic={ic} oc={ocs} K={Ks} cus={cus}")
 
 
+# ---------------------------------------------------------------- 5..16-row GEMV (gemv16)
+
+def gemv16(rl, rows, ic, ocs, Ks, cbs=None, cus=256):
+    cbs = cbs or [0] * len(ocs)
+    st = (ctypes.c_longlong * 4)()
+    rc = rl.exl3r_gemv16(rows, ic, len(ocs), _arr(ocs), _arr(Ks), _arr(cbs), cus, st)
+    return rc, rl.exl3r_message().decode(), list(st)
+
+
+@pytest.mark.parametrize("rows", [5, 9, 16])
+@pytest.mark.parametrize("cus", [256, 304, 8, 1])
+def test_gemv16_layers(rl, rows, cus):
+    ok(gemv16(rl, rows, 5120, *QKV, cus=cus), f"qkv rows={rows}")
+    ok(gemv16(rl, rows, 5120, *GATE_UP, cus=cus), f"gate_up rows={rows}")
+    ok(gemv16(rl, rows, 17408, [5120], [4], cus=cus), f"down_proj rows={rows}")
+    ok(gemv16(rl, rows, 6144, [5120], [4], cus=cus), f"o_proj rows={rows}")
+    ok(gemv16(rl, rows, 5120, [6144, 1024, 1024], [2, 3, 5], cus=cus), f"qkv three K rows={rows}")
+
+
+def test_gemv16_lm_head(rl):
+    ok(gemv16(rl, 16, 5120, [151936], [6]), "lm_head 16 rows")
+
+
+@pytest.mark.parametrize("K", range(1, 9))
+def test_gemv16_every_K(rl, K):
+    ok(gemv16(rl, 7, 768, [384, 128], [K, K], [0, 1]), f"K={K}")
+
+
+def test_gemv16_random_shapes(rl):
+    rnd = random.Random(1616)
+    for case in range(200):
+        ic = 128 * rnd.randint(1, 48)
+        n = rnd.randint(1, 9)
+        ocs = [128 * rnd.randint(1, 40) for _ in range(n)]
+        Ks = [rnd.randint(1, 8) for _ in range(n)]
+        cbs = [rnd.randint(0, 1) for _ in range(n)]
+        rows = rnd.randint(1, 16)
+        cus = rnd.choice(CUS + (2, 3, 33, 120))
+        ok(gemv16(rl, rows, ic, ocs, Ks, cbs, cus), f"case {case}: rows={rows} ic={ic} oc={ocs} K={Ks} cus={cus}")
+
+
 # ---------------------------------------------------------------- stream-K GEMM
 
 @pytest.mark.parametrize("rows", [17, 32, 40, 48, 64, 80, 96, 144, 300, 385, 2048])

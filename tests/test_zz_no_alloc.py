@@ -118,12 +118,12 @@ def test_static_under_graph_capture(native, oracle):
 def test_static_rejects_calls_above_its_scratch(native):
     """Host check only (no GPU call): a grouped call whose workspace exceeds the array."""
     L = native.lib()
-    arr = (native.Shard * 3)()
-    for i, oc in enumerate((syn.Q_OUT, syn.KV_OUT, syn.KV_OUT)):
-        arr[i] = native.Shard(0x10000, 0x10000, 0x10000, 0x10000, 8192, oc, 4, 0)
-    need = L.exl3_gemv_grouped_workspace_bytes(arr, 3, 16, syn.HIDDEN)
+    arr = (native.Shard * 4)()
+    for i in range(4):
+        arr[i] = native.Shard(0x10000, 0x10000, 0x10000, 0x10000, 4 * syn.INTERMEDIATE, syn.INTERMEDIATE, 4, 0)
+    need = L.exl3_gemv_grouped_workspace_bytes(arr, 4, 16, syn.HIDDEN)
     assert need > 16 << 20
-    rc = L.exl3_gemv_grouped_static(P(0x10000), arr, 3, 16, syn.HIDDEN, None)
+    rc = L.exl3_gemv_grouped_static(P(0x10000), arr, 4, 16, syn.HIDDEN, None)
     assert rc == 3
     msg = L.exl3_last_error().decode()
     assert "static" in msg and str(need) in msg
