@@ -45,12 +45,9 @@ int gemm_dispatch(const uint16_t* A, const uint32_t* trellis, uint16_t* C, const
                   const uint16_t* svh, void* workspace, size_t ws_bytes, int rows, int ic, int oc,
                   int K, int cb, hipStream_t stream);
 size_t gemm_sk_slot_bytes(int rows, int oc);
-size_t gemv_sk_bytes(int rows, int ic, int oc);
 size_t gemv16_shard_bytes(int ic, int oc);
 int gemv16_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws, size_t ws_bytes,
                     hipStream_t stream);
-int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws, size_t ws_bytes,
-                     hipStream_t stream);
 size_t gemm_grouped_shard_bytes(int rows, int ic, int oc);
 int gemm_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws,
                           size_t ws_bytes, hipStream_t stream);

@@ -1,10 +1,9 @@
-// EXL3 GEMM, stream-K over BM x 256 output tiles (BM = 32, 48, 64, 96, 128 or 256 for prefill by
-// row count, 16 for 5..16-row decode batches):
+// EXL3 GEMM, stream-K over BM x 256 output tiles (BM = 32, 48, 64, 96, 128 or 256 by row count):
 //   C = fp16( H( Ah . W_q ) * svh ),  Ah = fp16(H(A * suh)) (a had_r_128 pass)
 // W_q is decoded from the packed trellis straight into LDS (never written to HBM), once per
 // BM-row tile, and multiplied with v_mfma_f32_16x16x32_f16.  Replaces the reconstruct
 // branch of orcasaq2/ops.py:50-59 (reconstruct -> hgemm_recon -> had_r_128) for many rows,
-// and the fused exl3_gemm of orcasaq2/ops.py:46-49 for 2..16 rows.
+// and the fused exl3_gemm of orcasaq2/ops.py:46-49 for 17..GEMM_MAX_ROWS rows.
 //
 // Work decomposition.  Output tiles are BM rows x 256 outputs (two output Hadamard blocks);
 // a tile is nks = ic / 64 K-steps of 64 inputs.  The tiles' K-steps (all shards of a launch,
@@ -16,7 +15,7 @@
 // tile) adds the slots in workgroup order -- deterministic -- and finishes the tile.
 //
 // Per workgroup (8 waves; BM = 256: wave w owns rows 128 (w / 4) .., outputs 64 (w % 4) ..,
-// 8 x 4 MFMA blocks; BM = 16..128: wave w owns all rows and outputs 32 w .., BM/16 x 2
+// 8 x 4 MFMA blocks; BM = 32..128: wave w owns all rows and outputs 32 w .., BM/16 x 2
 // blocks) and K-step:
 //   * the A tile (BM x 64 fp16) is loaded into registers one K-step ahead, then stored to
 //     LDS rows of 72 halves (16-byte reads of 16 consecutive rows hit distinct banks);
@@ -128,8 +127,8 @@ __device__ __forceinline__ void sk_load(uint32_t (&w)[K + 1], const uint32_t* __
 
 // K > 0: every shard of the launch has K bits per weight; K = 0: each tile piece takes its
 // shard's K (one launch for shards of different bit widths).
-template <int K, int CB, int BM, int NBUF>
-__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(sk_wpe<BM, NBUF>(), sk_wpe<BM, NBUF>())))
+template <int K, int CB, int BM>
+__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(SK_WPE, SK_WPE)))
 void gemm_sk_kernel(const SkArgs a)
 {
     using Cfg = SkCfg<BM>;
@@ -219,41 +218,31 @@ void gemm_sk_kernel(const SkArgs a)
             };
 
 
+            // Software pipeline over two LDS buffers, one barrier per K-step: during step s the
+            // MFMAs read buffer (s - s0) % 2 while the step s + 1 tiles (loaded into registers a
+            // step earlier) are decoded into the other buffer and step s + 2 is loaded.  The step
+            // is one basic block (the last steps re-decode and re-load in-bounds data that is
+            // never read), so the scheduler can issue the decode's VALU work between the MFMAs,
+            // which run on the matrix pipe meanwhile.
             load_step(s0);
-            if constexpr (NBUF == 2) {
-                // Software pipeline over two LDS buffers, one barrier per K-step: during step s the
-                // MFMAs read buffer (s - s0) % 2 while the step s + 1 tiles (loaded into registers
-                // a step earlier) are decoded into the other buffer and step s + 2 is loaded.  The
-                // step is one basic block (the last steps re-decode and re-load in-bounds data that
-                // is never read), so the scheduler can issue the decode's VALU work between the
-                // MFMAs, which run on the matrix pipe meanwhile.
-                store_step(0);
-                load_step(min(s0 + 1, s1 - 1));
-                __syncthreads();
-                if (wave < SK_WAVES / 2) {
-                    for (int s = s0; s < s1; s++) {
-                        const int b = (s - s0) & 1;
-                        mfma_step(b);
-                        store_step(b ^ 1);
-                        load_step(min(s + 2, s1 - 1));
-                        __syncthreads();          // buffer b ^ 1 is complete; buffer b is free
-                    }
-                } else {
-                    for (int s = s0; s < s1; s++) {
-                        const int b = (s - s0) & 1;
-                        store_step(b ^ 1);
-                        load_step(min(s + 2, s1 - 1));
-                        mfma_step(b);
-                        __syncthreads();          // buffer b ^ 1 is complete; buffer b is free
-                    }
+            store_step(0);
+            load_step(min(s0 + 1, s1 - 1));
+            __syncthreads();
+            if (wave < SK_WAVES / 2) {
+                for (int s = s0; s < s1; s++) {
+                    const int b = (s - s0) & 1;
+                    mfma_step(b);
+                    store_step(b ^ 1);
+                    load_step(min(s + 2, s1 - 1));
+                    __syncthreads();          // buffer b ^ 1 is complete; buffer b is free
                 }
             } else {
                 for (int s = s0; s < s1; s++) {
-                    __syncthreads();              // the previous step's MFMAs are done with LDS
-                    store_step(0);
-                    __syncthreads();
-                    if (s + 1 < s1) load_step(s + 1);
-                    mfma_step(0);
+                    const int b = (s - s0) & 1;
+                    store_step(b ^ 1);
+                    load_step(min(s + 2, s1 - 1));
+                    mfma_step(b);
+                    __syncthreads();          // buffer b ^ 1 is complete; buffer b is free
                 }
             }
         };
@@ -410,22 +399,21 @@ int gemm_sk_cus()
 
 size_t gemm_sk_slot_bytes(int rows, int oc) { return sk_single_bytes(rows, oc, gemm_sk_cus()); }
 
-size_t gemv_sk_bytes(int rows, int ic, int oc) { return sk_grouped_bytes<16>(rows, ic, oc, gemm_sk_cus()); }
 
 size_t gemm_grouped_shard_bytes(int rows, int ic, int oc)
 {
     return sk_grouped_bytes_bm(gemm_sk_bm(rows), rows, ic, oc, gemm_sk_cus());
 }
 
-template <int K, int CB, int BM, int NBUF>
-static const void* sk_fn() { return reinterpret_cast<const void*>(&gemm_sk_kernel<K, CB, BM, NBUF>); }
+template <int K, int CB, int BM>
+static const void* sk_fn() { return reinterpret_cast<const void*>(&gemm_sk_kernel<K, CB, BM>); }
 
-template <int BM, int NBUF>
+template <int BM>
 static const void* sk_fn_kcb(int K, int cb)
 {
-#define EXL3_CASE(KK) case KK: return cb == CB_MCG ? sk_fn<KK, CB_MCG, BM, NBUF>() : sk_fn<KK, CB_3INST, BM, NBUF>();
+#define EXL3_CASE(KK) case KK: return cb == CB_MCG ? sk_fn<KK, CB_MCG, BM>() : sk_fn<KK, CB_3INST, BM>();
     if constexpr (sk_has_k0<BM>())
-        if (K == 0) return cb == CB_MCG ? sk_fn<0, CB_MCG, BM, NBUF>() : sk_fn<0, CB_3INST, BM, NBUF>();   // per-shard K
+        if (K == 0) return cb == CB_MCG ? sk_fn<0, CB_MCG, BM>() : sk_fn<0, CB_3INST, BM>();   // per-shard K
     switch (K) {
         EXL3_CASE(1) EXL3_CASE(2) EXL3_CASE(3) EXL3_CASE(4)
         EXL3_CASE(5) EXL3_CASE(6) EXL3_CASE(7) EXL3_CASE(8)
@@ -434,30 +422,28 @@ static const void* sk_fn_kcb(int K, int cb)
     return nullptr;
 }
 
-static const void* sk_fn_any(int BM, int NBUF, int K, int cb)
+static const void* sk_fn_any(int BM, int K, int cb)
 {
     switch (BM) {
-    case 16: return NBUF == 2 ? sk_fn_kcb<16, 2>(K, cb) : sk_fn_kcb<16, 1>(K, cb);
-    case 32: return sk_fn_kcb<32, 2>(K, cb);
-    case 48: return sk_fn_kcb<48, 2>(K, cb);
-    case 64: return sk_fn_kcb<64, 2>(K, cb);
-    case 96: return sk_fn_kcb<96, 2>(K, cb);
-    case 128: return sk_fn_kcb<128, 2>(K, cb);
-    case 256: return sk_fn_kcb<256, 2>(K, cb);
+    case 32: return sk_fn_kcb<32>(K, cb);
+    case 48: return sk_fn_kcb<48>(K, cb);
+    case 64: return sk_fn_kcb<64>(K, cb);
+    case 96: return sk_fn_kcb<96>(K, cb);
+    case 128: return sk_fn_kcb<128>(K, cb);
+    case 256: return sk_fn_kcb<256>(K, cb);
     }
     return nullptr;
 }
 
-static int sk_lds_any(int BM, int NBUF)
+static int sk_lds_any(int BM)
 {
     switch (BM) {
-    case 16: return NBUF == 2 ? sk_lds<16, 2>() : sk_lds<16, 1>();
-    case 32: return sk_lds<32, 2>();
-    case 48: return sk_lds<48, 2>();
-    case 64: return sk_lds<64, 2>();
-    case 96: return sk_lds<96, 2>();
-    case 128: return sk_lds<128, 2>();
-    default: return sk_lds<256, 2>();
+    case 32: return sk_lds<32>();
+    case 48: return sk_lds<48>();
+    case 64: return sk_lds<64>();
+    case 96: return sk_lds<96>();
+    case 128: return sk_lds<128>();
+    default: return sk_lds<256>();
     }
 }
 
@@ -476,9 +462,9 @@ static int sk_emit(const SkLaunch& L, const char* what, hipStream_t stream)
         const int rc = check_launch(what);
         if (rc != EXL3_OK) return rc;
     }
-    const void* fn = sk_fn_any(L.BM, L.NBUF, L.K, L.cb);
+    const void* fn = sk_fn_any(L.BM, L.K, L.cb);
     if (!fn) return set_error(EXL3_ERR_ARG, "%s: K=%d is not in 1..8", what, L.K);   // K = 0: per shard
-    const int lds = sk_lds_any(L.BM, L.NBUF);
+    const int lds = sk_lds_any(L.BM);
     if (lds > 64 * 1024) {
         hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
         (void)hipGetLastError();
@@ -501,13 +487,6 @@ static int sk_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int n
 {
     return sk_plan_grouped<BM>(A, shards, nshards, rows, ws, ws_bytes, what, gemm_sk_cus(),
                                [&](const SkLaunch& L) { return sk_emit(L, what, stream); });
-}
-
-// 2..16 rows: 16-row tiles.
-int gemv_sk_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws, size_t ws_bytes,
-                     hipStream_t stream)
-{
-    return sk_grouped_dispatch<16>(A, shards, nshards, rows, ws, ws_bytes, "exl3_gemv", stream);
 }
 
 // Prefill of several shards (exl3_gemm_grouped): tile height by rows, as for one shard.

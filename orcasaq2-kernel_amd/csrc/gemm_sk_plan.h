@@ -23,7 +23,7 @@ constexpr int SK_KS = 64;                     // inputs per K-step (4 tile rows)
 constexpr int SK_LD = SK_KS + 8;              // halves per LDS row of the A and B tiles
 constexpr int SK_CLD = 128 + 4;               // floats per epilogue row in LDS (BM = 256)
 constexpr int SK_MAXSH = 8;                   // shards per launch
-constexpr int SK_PIPE16 = 24;                 // 16-row launches up to this many K-steps per CU: two buffers
+constexpr int SK_WPE = 2;                     // waves per SIMD the register budget is set for (one workgroup per CU)
 
 // Wave grid of a BM x 256 tile: WM x WN waves, each MB x NB blocks of 16 x 16.
 template <int BM>
@@ -40,28 +40,17 @@ template <>
 struct SkCfg<48> { static constexpr int WM = 1, WN = 8, MB = 3, NB = 2; };
 template <>
 struct SkCfg<32> { static constexpr int WM = 1, WN = 8, MB = 2, NB = 2; };
-template <>
-struct SkCfg<16> { static constexpr int WM = 1, WN = 8, MB = 1, NB = 2; };
 
 template <int BM>
 constexpr int sk_acc() { return SkCfg<BM>::MB * SkCfg<BM>::NB * 4; }   // fp32 accumulators per lane
-// LDS of a launch: the A and B tiles of one K-step, twice for BM >= 32 (the tiles of step
-// s + 1 are written while the MFMAs read those of step s; one workgroup per CU), once for
-// BM = 16 (three workgroups per CU overlap one another's phases instead).  Measured on
-// MI355X at 17..64 rows: the two-buffer pipeline with one workgroup per CU beats one buffer
-// with two workgroups per CU by 28% on 17408 -> 5120 and 6% on 5120 -> 17408.
-// A 16-row launch takes either form (NBUF = 1 or 2, chosen by its length).
-template <int BM>
-constexpr int sk_nbuf() { return BM >= 32 ? 2 : 1; }
-// Waves per SIMD the register budget is set for, and workgroups per CU of a launch.
-template <int BM, int NBUF>
-constexpr int sk_wpe() { return NBUF == 2 ? 2 : 6; }
-template <int BM, int NBUF>
-constexpr int sk_wgpc() { return NBUF == 2 ? 1 : 3; }
+// LDS of a launch: the A and B tiles of one K-step, twice (the tiles of step s + 1 are written
+// while the MFMAs read those of step s), one workgroup per CU.  Measured on MI355X at 17..64
+// rows: the two-buffer pipeline with one workgroup per CU beats one buffer with two
+// workgroups per CU by 28% on 17408 -> 5120 and 6% on 5120 -> 17408.
 template <int BM>
 constexpr int sk_buf() { return (BM + SK_BN) * SK_LD; }                   // halves per A + B buffer
-template <int BM, int NBUF>
-constexpr int sk_lds() { return NBUF * sk_buf<BM>() * 2; }      // bytes
+template <int BM>
+constexpr int sk_lds() { return 2 * sk_buf<BM>() * 2; }      // bytes
 
 struct SkShard {
     const uint16_t* Ah;        // (rows, ic) fp16, fp16(H(A * suh)) of this shard
@@ -222,9 +211,9 @@ SK_HD int sk_cx(int row, int col) { return row * (SK_BN + 4) + col; }
 
 inline size_t sk_align(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// Workgroups per launch: sk_wgpc per CU, all resident at once.
-template <int BM, int NBUF = sk_nbuf<BM>()>
-inline int sk_gmax(int cus) { return sk_wgpc<BM, NBUF>() * cus; }
+// Workgroups per launch: one per CU, all resident at once.
+template <int BM>
+inline int sk_gmax(int cus) { return cus; }
 
 template <int BM>
 inline size_t sk_slot_bytes() { return (size_t)SK_WAVES * sk_acc<BM>() * 64 * sizeof(float); }
@@ -278,7 +267,6 @@ inline size_t sk_grouped_bytes(int rows, int ic, int oc, int cus)
 inline size_t sk_grouped_bytes_bm(int bm, int rows, int ic, int oc, int cus)
 {
     switch (bm) {
-    case 16: return sk_grouped_bytes<16>(rows, ic, oc, cus);
     case 32: return sk_grouped_bytes<32>(rows, ic, oc, cus);
     case 48: return sk_grouped_bytes<48>(rows, ic, oc, cus);
     case 96: return sk_grouped_bytes<96>(rows, ic, oc, cus);
@@ -295,7 +283,7 @@ constexpr bool sk_has_k0() { return BM <= 128; }
 
 // One stream-K launch of the plan.
 struct SkLaunch {
-    int BM, NBUF, K, cb, G;      // K = 0: each tile piece takes its shard's K
+    int BM, K, cb, G;            // K = 0: each tile piece takes its shard's K
     bool clear;                  // clear the tile counters with a fill kernel first
     bool prep;                   // the set-up kernel (prep) runs first
     long prep_waves;
@@ -348,7 +336,6 @@ int sk_plan_single(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, con
     a.ntiles = ((rows + bm - 1) / bm) * s.ntn;
     SkLaunch L = {};
     L.BM = bm;
-    L.NBUF = bm >= 32 ? 2 : 1;
     L.K = K;
     L.cb = cb;
     L.clear = true;
@@ -370,10 +357,7 @@ int sk_plan_single(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, con
 // Shards that read the same A (rows x ic): per codebook (and per K where no per-piece-K
 // kernel exists), groups of up to SK_MAXSH shards; per group one set-up kernel (the
 // shards' activations, the group's tile counters) and one stream-K launch -- a single-K
-// kernel when the group's shards share K, else the per-shard-K one.  16-row tiles: a short
-// launch (at most SK_PIPE16 K-steps per CU) takes the two-buffer pipeline with one workgroup
-// per CU, a longer one three single-buffer workgroups per CU (measured on MI355X at 16 rows:
-// qkv, ~10 K-steps per CU, 31 -> 26 us; gate_up, ~42 per CU, 56 -> 62 us with two buffers).
+// kernel when the group's shards share K, else the per-shard-K one.
 template <int BM, class Emit>
 int sk_plan_grouped(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws, size_t ws_bytes,
                     const char* what, int cus, Emit&& emit)
@@ -431,15 +415,7 @@ int sk_plan_grouped(const uint16_t* A, const GemvShard* shards, int nshards, int
         L.prep_args = &p;
         const size_t need = sk_ws<BM>(tiles, sk_gmax<BM>(cus));
         const size_t avail = ws_bytes > off ? ws_bytes - off : 0;
-        int rc;
-        if constexpr (BM == 16) {
-            L.NBUF = (long)tiles * a.nks <= (long)SK_PIPE16 * cus ? 2 : 1;
-            rc = L.NBUF == 2 ? sk_place<16>(a, sk_gmax<16, 2>(cus), ws + off, std::min(need, avail), what, L.G)
-                             : sk_place<16>(a, sk_gmax<16, 1>(cus), ws + off, std::min(need, avail), what, L.G);
-        } else {
-            L.NBUF = sk_nbuf<BM>();
-            rc = sk_place<BM>(a, sk_gmax<BM>(cus), ws + off, std::min(need, avail), what, L.G);
-        }
+        int rc = sk_place<BM>(a, sk_gmax<BM>(cus), ws + off, std::min(need, avail), what, L.G);
         if (rc != EXL3_OK) return rc;
         rc = emit(static_cast<const SkLaunch&>(L));
         if (rc != EXL3_OK) return rc;

@@ -474,12 +474,12 @@ int sk_shard_index(const SkWorld& W, const GemvShard* shards, const uint32_t* tr
 
 // The LDS tiles of a BM-row launch: every A / B element the MFMAs read is one a store wrote,
 // and all accesses stay in their buffer's tile (independent of the piece, so checked once).
-template <int BM, int NBUF>
+template <int BM>
 void sk_check_lds()
 {
     constexpr int MB = SkCfg<BM>::MB, NB = SkCfg<BM>::NB, AP = (BM + 63) / 64;
-    const int lds_halves = sk_lds<BM, NBUF>() / 2;
-    for (int b = 0; b < NBUF; b++) {
+    const int lds_halves = sk_lds<BM>() / 2;
+    for (int b = 0; b < 2; b++) {
         std::vector<uint8_t> aw((size_t)BM * SK_KS, 0), bw((size_t)SK_BN * SK_KS, 0);
         for (int tid = 0; tid < 64 * SK_WAVES; tid++) {
             const int arow = sk_arow(tid), aseg = sk_aseg(tid);
@@ -519,7 +519,7 @@ void sk_check_lds()
         }
     }
     // epilogue staging
-    const int lds_floats = sk_lds<BM, NBUF>() / 4;
+    const int lds_floats = sk_lds<BM>() / 4;
     for (int wave = 0; wave < SK_WAVES; wave++) {
         const int wm = wave / SkCfg<BM>::WN, wn = wave % SkCfg<BM>::WN;
         for (int lane = 0; lane < 64; lane++)
@@ -535,7 +535,7 @@ void sk_check_lds()
 
 // One BM-row launch (after the clear or set-up kernel): every workgroup's pieces, their loads,
 // slot traffic and epilogue stores.
-template <int BM, int NBUF>
+template <int BM>
 void sk_replay_launch(SkWorld& W, const GemvShard* shards, const SkLaunch& L, int launch)
 {
     constexpr int MB = SkCfg<BM>::MB, NB = SkCfg<BM>::NB, AP = (BM + 63) / 64;
@@ -545,7 +545,7 @@ void sk_replay_launch(SkWorld& W, const GemvShard* shards, const SkLaunch& L, in
     if (G < 1) fail("launch %d: %d workgroups", launch, G);
     if (sk_first(a, G) != units) fail("launch %d: ranges end at %ld, not %ld", launch, sk_first(a, G), units);
     if (a.q < 1) fail("launch %d: %d K-steps per workgroup", launch, a.q);
-    sk_check_lds<BM, NBUF>();
+    sk_check_lds<BM>();
     // counters and slots inside the workspace share of this launch
     ws_region(W, a.counters, (long)a.ntiles * 4, "tile counters");
     const long slot_floats = (long)(a.ntiles + G) * SK_WAVES * sk_acc<BM>() * 64;
@@ -645,13 +645,8 @@ void sk_replay_launch(SkWorld& W, const GemvShard* shards, const SkLaunch& L, in
             };
             // the kernel's load order
             load_step(pc.s0);
-            if (NBUF == 2) {
-                load_step(std::min(pc.s0 + 1, pc.s1 - 1));
-                for (int st = pc.s0; st < pc.s1; st++) load_step(std::min(st + 2, pc.s1 - 1));
-            } else {
-                for (int st = pc.s0; st < pc.s1; st++)
-                    if (st + 1 < pc.s1) load_step(st + 1);
-            }
+            load_step(std::min(pc.s0 + 1, pc.s1 - 1));
+            for (int st = pc.s0; st < pc.s1; st++) load_step(std::min(st + 2, pc.s1 - 1));
             W.pieces++;
             u += pc.s1 - pc.s0;
             if (pc.s0 == 0 && pc.s1 == a.nks) {
@@ -724,19 +719,15 @@ void sk_replay_any(SkWorld& W, const GemvShard* shards, const SkLaunch& L, int l
 {
     if (L.prep) sk_replay_prep(W, shards, L);
     switch (L.BM) {
-    case 16:
-        if (L.NBUF == 2) sk_replay_launch<16, 2>(W, shards, L, launch);
-        else sk_replay_launch<16, 1>(W, shards, L, launch);
-        break;
-    case 32: sk_replay_launch<32, 2>(W, shards, L, launch); break;
-    case 48: sk_replay_launch<48, 2>(W, shards, L, launch); break;
-    case 64: sk_replay_launch<64, 2>(W, shards, L, launch); break;
-    case 96: sk_replay_launch<96, 2>(W, shards, L, launch); break;
-    case 128: sk_replay_launch<128, 2>(W, shards, L, launch); break;
-    case 256: sk_replay_launch<256, 2>(W, shards, L, launch); break;
+    case 32: sk_replay_launch<32>(W, shards, L, launch); break;
+    case 48: sk_replay_launch<48>(W, shards, L, launch); break;
+    case 64: sk_replay_launch<64>(W, shards, L, launch); break;
+    case 96: sk_replay_launch<96>(W, shards, L, launch); break;
+    case 128: sk_replay_launch<128>(W, shards, L, launch); break;
+    case 256: sk_replay_launch<256>(W, shards, L, launch); break;
     default: fail("tile height %d", L.BM);
     }
-    if (L.K == 0 && !sk_has_k0<256>() && L.BM == 256) fail("per-shard-K launch of 256-row tiles");
+    if (L.K == 0 && L.BM == 256) fail("per-shard-K launch of 256-row tiles");
 }
 
 
@@ -993,31 +984,31 @@ int exl3r_gemv1(int rows, int ic, int nshards, const int* oc, const int* K, cons
 }
 
 
-// The stream-K GEMM for nshards shards sharing ic: mode 0 = exl3_gemm (one shard, tile height
-// by rows), 1 = exl3_gemm_grouped (tile height by rows), 2 = exl3_gemv's 5..16-row path
-// (16-row tiles).  Workspaces are sized as the product sizes them for `cus` CUs.  Returns as
-// exl3r_gemv1; stats: launches, K-step loads checked, pieces, slot stores.
+// The stream-K GEMM for nshards shards sharing ic: mode 0 = exl3_gemm (one shard), 1 =
+// exl3_gemm_grouped; tile height by rows.  Workspaces are sized as the product sizes them for
+// `cus` CUs.  Returns as exl3r_gemv1; stats: launches, K-step loads checked, pieces, slot
+// stores.
 int exl3r_gemm_sk(int mode, int rows, int ic, int nshards, const int* oc, const int* K, const int* cb, int cus,
                   long long* stats)
 {
     g_msg.clear();
     try {
-        if (nshards < 1 || nshards > EXL3_MAX_SHARDS || (mode == 0 && nshards != 1)) fail("nshards %d", nshards);
+        if (nshards < 1 || nshards > EXL3_MAX_SHARDS || (mode == 0 && nshards != 1) || mode < 0 || mode > 1)
+            fail("mode %d, nshards %d", mode, nshards);
         SkWorld W;
         W.rows = rows;
         W.ic = ic;
         std::vector<GemvShard> shards(nshards);
         long cols = 0;
         size_t ws = 0;
-        const int bm = mode == 2 ? 16 : gemm_sk_bm(rows);
+        const int bm = gemm_sk_bm(rows);
         for (int i = 0; i < nshards; i++) {
             W.sh.push_back(ShardSpec{ic, oc[i], K[i], cb[i]});
             W.col0.push_back((int)cols);
             W.ah_buf.push_back(mode == 0 ? B_AH + i : -1);
             cols += oc[i];
             if (mode == 0) ws += sk_single_bytes(rows, oc[i], cus);
-            else if (mode == 1) ws += sk_grouped_bytes_bm(bm, rows, ic, oc[i], cus);
-            else ws += sk_align(sk_grouped_bytes<16>(rows, ic, oc[i], cus));
+            else ws += sk_grouped_bytes_bm(bm, rows, ic, oc[i], cus);
         }
         W.ldc = cols;
         W.ws_bytes = ws;
@@ -1044,9 +1035,8 @@ int exl3r_gemm_sk(int mode, int rows, int ic, int nshards, const int* oc, const 
             rc = sk_plan_single(fake_ptr<uint16_t>(B_AH), shards[0].trellis, shards[0].C, shards[0].svh, fake_ptr<char>(B_WS),
                                 ws, rows, ic, oc[0], K[0], cb[0], cus, emit);
         } else {
-            const char* what = mode == 1 ? "exl3_gemm_grouped" : "exl3_gemv";
+            const char* what = "exl3_gemm_grouped";
             switch (bm) {
-            case 16: rc = sk_plan_grouped<16>(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, what, cus, emit); break;
             case 32: rc = sk_plan_grouped<32>(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, what, cus, emit); break;
             case 48: rc = sk_plan_grouped<48>(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, what, cus, emit); break;
             case 64: rc = sk_plan_grouped<64>(fake_ptr<uint16_t>(B_X), shards.data(), nshards, rows, fake_ptr<char>(B_WS), ws, what, cus, emit); break;
