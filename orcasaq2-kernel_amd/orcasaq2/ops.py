@@ -8,14 +8,16 @@ kernels only enqueue on the current stream, so it can be captured in a HIP graph
 Dispatch on the number of activation rows (reference: orcasaq2/ops.py:25, 46-59):
   * rows <= 16            fused decode-GEMV (exl3_gemv): packed words streamed from HBM and
                           decoded in registers, never stored; rows 1..4: one persistent kernel
-                          (MFMA multiply-accumulate, split reduction fused in; rows 2..4 take
-                          MFMA partial sums + a reduce kernel where that kernel's LDS would not
-                          keep enough workgroups resident); rows 5..16: stream-K over 16-row
-                          tiles; output Hadamard and svh in the last step;
+                          (MFMA multiply-accumulate, split column groups finished by a second
+                          kernel; rows 2..4 of very wide shards take MFMA partial sums + a
+                          reduce kernel); rows 5..16: the same decode on 4 x 2-tile units, one
+                          MFMA serving all rows; output Hadamard and svh at the end;
   * 16 < rows <= GEMM_MAX_ROWS
                           fused decode-GEMM (exl3_gemm): Hadamard pass over x, then stream-K
                           tiles decoded straight into MFMA operands, output Hadamard in the
-                          epilogue; a fused layer's shards together (shards_gemm);
+                          epilogue; a fused layer's shards together (shards_gemm) -- except a
+                          single shard with 4096 <= ic < 8192 above 64 rows where the
+                          reconstruct branch measured faster (_fused_gemm_faster);
   * rows > GEMM_MAX_ROWS  the reference's reconstruct branch: had_r_128(x, suh), dense W_q
                           (decoded transposed, (oc, ic)) into a scratch freed on exit, library
                           fp16 transposed-B GEMM, had_r_128(y, svh).
@@ -43,6 +45,20 @@ def exl3_K(trellis: Tensor):
     return int(k) if float(k).is_integer() else k
 
 
+def _fused_gemm_faster(rows: int, ic: int, oc: int) -> bool:
+    """Whether the fused decode-GEMM beats the reconstruct branch for one shard at
+    GEMV_MAX_ROWS < rows <= GEMM_MAX_ROWS.  Measured on MI355X (us per call, HIP graph,
+    fused / reconstruct branch): 17408 -> 5120 wins at every row count to 768 (144 rows:
+    121 / 178); 5120 -> 17408 wins to 128 rows (81 / 87) and loses at 144 (117 / 99);
+    5120 -> 6144 ties at 64 (47 / 46) and loses from 80 (60 / 49) to 144 (71 / 54).  With
+    ic in [4096, 8192) the dense W_q is cheap to rebuild and the library GEMM short, so above
+    64 rows the branch wins unless oc is at least twice ic and rows stay within 128; other
+    input widths (unmeasured below 4096) keep the fused path."""
+    if rows <= 64 or ic >= 8192 or ic < 4096:
+        return True
+    return rows <= 128 and oc >= 2 * ic
+
+
 def _shard_gemm_impl(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, oc: int, k: float,
                      mcg: bool, mul1: bool) -> Tensor:
     cb = _native.codebook_id(mcg, mul1)
@@ -53,7 +69,7 @@ def _shard_gemm_impl(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, oc: i
         return x.new_empty((0, oc), dtype=torch.half)
     if rows <= GEMV_MAX_ROWS:
         return _native.gemv(x, trellis, suh, svh, k, cb)
-    if rows <= GEMM_MAX_ROWS:
+    if rows <= GEMM_MAX_ROWS and _fused_gemm_faster(rows, ic, oc):
         return _native.gemm(x, trellis, suh, svh, k, cb)
     # reconstruct branch: dense W_q lives only for the duration of the call, decoded as
     # W_q^T (oc, ic) so the library runs its transposed-B GEMM (measured 15-20% faster than

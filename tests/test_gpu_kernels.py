@@ -207,6 +207,24 @@ def test_gemv1_workgroup_ranges(native, oracle, ic, ocs, K, rows):
         col += l["oc"]
 
 
+@pytest.mark.parametrize("ic,ocs,K", [(128, [131200], 2), (256, [384, 128, 640], 3), (384, [1152], 5),
+                                      (2048, [128], 4), (256, [2048, 2048], 4), (640, [128, 256, 128], 6)])
+@pytest.mark.parametrize("rows", [7, 13])
+def test_gemv16_workgroup_ranges(native, oracle, ic, ocs, K, rows):
+    """5..16 rows (gemv16.hip) on the range-boundary shapes of the 1..4-row test: ranges that
+    span several strips and shards, start inside a strip, or cover a whole launch; strips with
+    one and with many contributing workgroups."""
+    x = syn.activations(rows, ic, torch.Generator().manual_seed(ic + K + rows))
+    lins = [syn.linear(ic, oc, K, seed=350 + i) for i, oc in enumerate(ocs)]
+    shards = [dict(to_gpu(l), codebook=0) for l in lins]
+    y = native.gemv_grouped(x.to(dev()), shards)
+    col = 0
+    for l in lins:
+        check_linear_out(y[:, col:col + l["oc"]], x, l, 0, oracle)
+        col += l["oc"]
+    assert torch.equal(native.gemv_grouped(x.to(dev()), shards), y)
+
+
 @pytest.mark.parametrize("rows", [1, 3, 9])
 def test_gemv_grouped_mixed_K_and_codebooks(native, oracle, rows):
     """Shards of several K (interleaved, so a group is not a contiguous run of shards) and

@@ -25,6 +25,8 @@ def ref(oracle, x, lin, cb=0):
 
 @pytest.mark.parametrize("rows", [1, 16, 17, 144, 145, 400])
 def test_shard_gemm_branches(native, oracle, rows):
+    """1 and 16 rows: fused GEMV; 17 and 144: fused GEMM (ic = 512 keeps it); 145 and 400:
+    the reconstruct branch."""
     lin = syn.linear(512, 256, 4, seed=rows)
     x = syn.activations(rows, 512, torch.Generator().manual_seed(rows))
     d = on(lin)
@@ -48,6 +50,20 @@ def test_shard_gemm_wrong_width_message(native):
     x = torch.zeros(1, 256, dtype=torch.half, device=D)
     with pytest.raises(RuntimeError, match="packed dimension 2 is incorrect size"):
         torch.ops.orcasaq2.shard_gemm(x, lin["trellis"], lin["suh"], lin["svh"], 256, 3.0, False, False)
+
+
+@pytest.mark.parametrize("rows,oc", [(80, 1024), (144, 1024), (120, 10240)])
+def test_shard_gemm_routing_by_shape(native, oracle, rows, oc):
+    """5120-input shards above 64 rows: the reconstruct branch where it measured faster (oc <
+    2 ic, or more than 128 rows), the fused GEMM for wide outputs up to 128 rows; both match
+    the oracle."""
+    ic = 5120
+    assert O._fused_gemm_faster(rows, ic, oc) == (oc >= 2 * ic and rows <= 128)
+    lin = syn.linear(ic, oc, 3, seed=rows + oc)
+    x = syn.activations(rows, ic, torch.Generator().manual_seed(rows))
+    d = on(lin)
+    y = torch.ops.orcasaq2.shard_gemm(x.to(D), d["trellis"], d["suh"], d["svh"], oc, 3.0, False, False)
+    assert oracle.rel_err_rows(y.cpu().numpy(), ref(oracle, x, lin)).max() <= 1e-3
 
 
 def _two_shard_step(rows, ic=1024):

@@ -234,3 +234,15 @@ def test_product_op_has_no_cpu_path_without_the_test_kernel():
     r = subprocess.run([sys.executable, "-c", code], cwd=root, capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "NotImplementedError" in r.stdout or "RuntimeError" in r.stdout
+
+
+def test_fused_gemm_routing_follows_the_measured_crossovers():
+    """The op's choice between the fused decode-GEMM and the reconstruct branch at 17..144
+    rows, on the shapes whose crossovers were measured (orcasaq2.ops._fused_gemm_faster)."""
+    from orcasaq2 import ops
+    f = ops._fused_gemm_faster
+    for rows in (17, 64, 80, 128, 144):
+        assert f(rows, 17408, 5120)                    # down_proj: fused at every row count
+    assert f(64, 5120, 6144) and not f(80, 5120, 6144) and not f(144, 5120, 6144)   # q / o-like
+    assert f(128, 5120, 17408) and not f(144, 5120, 17408)                           # gate / up
+    assert f(144, 512, 256) and f(144, 2048, 1024)     # unmeasured narrow inputs keep the fused path
