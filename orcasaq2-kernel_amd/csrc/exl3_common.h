@@ -438,35 +438,56 @@ __device__ __forceinline__ float fwht_partner(float v)
         return __shfl_xor(v, D, 64);
 }
 
+// Per-lane butterfly signs of the six cross-lane rounds (round i pairs lane with lane ^ 2^i):
+// +1 in the lower lane of a pair, -1 in the upper.  Two VALU instructions each.
+struct FwhtSigns {
+    float s[6];
+};
+
+__device__ __forceinline__ FwhtSigns fwht_signs(int lane)
+{
+    FwhtSigns f;
+#pragma unroll
+    for (int i = 0; i < 6; i++)
+        f.s[i] = __builtin_bit_cast(float, 0x3f800000u | (((uint32_t)lane << (31 - i)) & 0x80000000u));
+    return f;
+}
+
 template <int D>
-__device__ __forceinline__ void fwht_round(float& v0, float& v1, int lane)
+__device__ __forceinline__ void fwht_round(float& v0, float& v1, float sg)
 {
     // lower lane: v + partner, upper lane: partner - v -- one fma with a +-1 factor each
     // (the same single rounding as the add or the subtraction)
-    const float sg = (lane & D) ? -1.f : 1.f;
     const float p0 = fwht_partner<D>(v0), p1 = fwht_partner<D>(v1);
     v0 = __builtin_fmaf(sg, v0, p0);
     v1 = __builtin_fmaf(sg, v1, p1);
 }
 
-__device__ __forceinline__ void wave_fwht128(float& v0, float& v1)
+// With the signs computed once by the caller: for loops of many transforms whose sign
+// registers are dead before any long loop that follows.
+__device__ __forceinline__ void wave_fwht128(float& v0, float& v1, const FwhtSigns& f)
 {
-    // The empty asm keeps the per-lane signs below from being hoisted out of the caller's
-    // loops (six more live registers across a persistent kernel's main loop).
-    int lane = threadIdx.x & 63;
-    asm volatile("" : "+v"(lane));
     float a = v0 + v1, b = v0 - v1;
     v0 = a;
     v1 = b;
-    fwht_round<1>(v0, v1, lane);
-    fwht_round<2>(v0, v1, lane);
-    fwht_round<4>(v0, v1, lane);
-    fwht_round<8>(v0, v1, lane);
-    fwht_round<16>(v0, v1, lane);
-    fwht_round<32>(v0, v1, lane);
+    fwht_round<1>(v0, v1, f.s[0]);
+    fwht_round<2>(v0, v1, f.s[1]);
+    fwht_round<4>(v0, v1, f.s[2]);
+    fwht_round<8>(v0, v1, f.s[3]);
+    fwht_round<16>(v0, v1, f.s[4]);
+    fwht_round<32>(v0, v1, f.s[5]);
     const float norm = 0.08838834764831845f;  // 1/sqrt(128)
     v0 *= norm;
     v1 *= norm;
+}
+
+__device__ __forceinline__ void wave_fwht128(float& v0, float& v1)
+{
+    // The empty asm keeps the per-lane signs from being hoisted out of the caller's loops
+    // (six more live registers across a persistent kernel's main loop).
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
+    wave_fwht128(v0, v1, fwht_signs(lane));
 }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(const f16x8& a, const f16x8& b, const f32x4& c)

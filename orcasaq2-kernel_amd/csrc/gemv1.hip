@@ -3,7 +3,7 @@
 // with W_q decoded from the packed trellis in registers and never stored.  Replaces
 // exllamav3_ext.exl3_gemm as called at orcasaq2/ops.py:46-49 for rows <= 4 (rows 2..4 only
 // where the launch keeps three workgroups per CU resident; gemv.hip's split kernels take
-// the rest, gemm_sk.hip's 16-row tiles take 5..16 rows).
+// the rest, gemv16.hip takes 5..16 rows).
 //
 // Work decomposition.  A *unit* is one tile row of one 128-output column group: 8 tiles
 // side by side, 64 chunks of 32 positions -- one chunk per lane of a wave, the 8 tiles'
@@ -157,37 +157,45 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     float* red = reinterpret_cast<float*>(lds);
     uint32_t* act = lds + ll.act;
     uint32_t* zero = lds + ll.zero;
-    if (threadIdx.x < 16) zero[threadIdx.x] = 0u;
+    if (threadIdx.x < g1_zero_words(nr)) zero[threadIdx.x] = 0u;
     const Dot2Consts kc = dot2_consts();
 
     // Activations, once per workgroup: the waves share out the (occurrence, activation row)
     // pairs; each transforms one block of one row, fp16(H128(x_r * suh)) (lane l: outputs 2l,
     // 2l + 1 = rows 2(l % 8), 2(l % 8) + 1 of the block's tile row l / 8) and stores each
     // output as a duplicated fp16 pair in the order the MFMAs read them (g1_act_word).  A wave
-    // issues the loads of up to G1_TBATCH of its pairs before transforming any of them.
+    // issues the loads of up to G1_TBATCH of its pairs before transforming any of them.  The
+    // task cursor steps without dividing, and the shard's suh pointer is read again only when
+    // the shard changes: the scalar unit is shared by every wave of the CU, and all of them
+    // run this loop at once.
     const int ntask = w.nocc * nr;
-    for (int t0 = wave; t0 < ntask; t0 += G1_NW * G1_TBATCH) {
+    const FwhtSigns fs = fwht_signs(lane);
+    const G1TaskStep tst = g1_task_step(nr);
+    G1Task tk = g1_task_first<ONE>(a, sht, w, wave, nr);
+    int s_suh = tk.s;
+    const uint16_t* suh = sh(s_suh).suh;
+    while (tk.t < ntask) {
         uint32_t sw[G1_TBATCH], xw[G1_TBATCH];
+        G1Task tb[G1_TBATCH];
 #pragma unroll
         for (int j = 0; j < G1_TBATCH; j++) {
-            const int t = t0 + j * G1_NW;
-            if (t < ntask) {
-                const int i = R == 1 ? t : t / nr, r = t - i * nr;
-                int k, blk;
-                g1_occ_block(a, w, i, k, blk);
-                const int s = g1_shard_of_seg<ONE>(a, sht, w.S_first + k);
-                sw[j] = reinterpret_cast<const uint32_t*>(sh(s).suh + blk * 128)[lane];
-                xw[j] = reinterpret_cast<const uint32_t*>(a.x + g1_x_elem(a, r, blk))[lane];
+            tb[j] = tk;
+            if (tk.t < ntask) {
+                if (tk.s != s_suh) {
+                    s_suh = tk.s;
+                    suh = sh(s_suh).suh;
+                }
+                sw[j] = reinterpret_cast<const uint32_t*>(suh + tk.blk * 128)[lane];
+                xw[j] = reinterpret_cast<const uint32_t*>(a.x + g1_x_elem(a, tk.r, tk.blk))[lane];
+                g1_task_next<ONE>(a, sht, w, tk, nr, tst);
             }
         }
 #pragma unroll
         for (int j = 0; j < G1_TBATCH; j++) {
-            const int t = t0 + j * G1_NW;
-            if (t < ntask) {
-                const int i = R == 1 ? t : t / nr, r = t - i * nr;
+            if (tb[j].t < ntask) {
                 float v0 = g1_lo(xw[j]) * g1_lo(sw[j]), v1 = g1_hi(xw[j]) * g1_hi(sw[j]);
-                wave_fwht128(v0, v1);
-                *reinterpret_cast<uint2*>(act + g1_act_word(i, lane, nr, r)) = uint2{g1_dup(v0), g1_dup(v1)};
+                wave_fwht128(v0, v1, fs);
+                *reinterpret_cast<uint2*>(act + g1_act_word(tb[j].i, lane, nr, tb[j].r)) = uint2{g1_dup(v0), g1_dup(v1)};
             }
         }
     }
@@ -213,6 +221,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     const int yrow = g1_yrow(lane), ycol = g1_ycol(lane);
     const uint32_t asel = g1_asel(lane);
     const uint32_t aoff = g1_aoff(lane, nr, ll);
+    constexpr int CH = g1_a_chunk(R == 1 ? 1 : G1_ROWS) / 16;   // f16x8 steps between A chunks
     int cur = cu.S - w.S_first;
     int occ = g1_occ_of(w, cur, cu.tr);
     const int pq1 = (n + 3) >> 2, pq2 = (n + 1) >> 1, pq3 = (3 * n + 3) >> 2;
@@ -235,7 +244,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
                 if (cu.S - w.S_first != cur) flush(cu.S - w.S_first);
                 const uint32_t e = g1_a_entry(occ, cu.tr, nr);
                 const f16x8* ap = reinterpret_cast<const f16x8*>(reinterpret_cast<const char*>(lds) + (__umul24(e, asel) + aoff));
-                const f16x8 av[4] = {ap[0], ap[1], ap[2], ap[3]};
+                const f16x8 av[4] = {ap[0], ap[CH], ap[2 * CH], ap[3 * CH]};
                 chunk_prev_dpp<K>(ring[d].w, first_lane);
                 g1_mfma_chunk<K, CB>(ring[d].w, av, yacc, kc);
                 if (j + d + 1 < n) {

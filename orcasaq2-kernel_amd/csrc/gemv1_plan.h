@@ -282,6 +282,68 @@ G1_HD void g1_occ_block(const G1Group& a, const G1Range& w, int i, int& k, int& 
     }
 }
 
+// A wave's activation-table tasks: the (occurrence i, activation row r) pairs t = i nr + r,
+// t = wave, wave + G1_NW, ...  The cursor steps by G1_NW tasks (= q nr + rm) with no
+// division and carries the occurrence's segment k, block blk (g1_occ_block), shard s and
+// the first segment of shard s + 1 (nxt; INT_MAX past the last shard).
+struct G1Task {
+    int t, i, r, k, blk, s, nxt;
+};
+
+struct G1TaskStep {
+    int q, rm;
+};
+
+G1_HD G1TaskStep g1_task_step(int nr)
+{
+    G1TaskStep st{0, G1_NW};
+    while (st.rm >= nr) {
+        st.rm -= nr;
+        st.q++;
+    }
+    return st;
+}
+
+template <bool ONE>
+G1_HD G1Task g1_task_first(const G1Group& a, const G1Shard* sht, const G1Range& w, int wave, int nr)
+{
+    G1Task c{wave, 0, wave, 0, 0, 0, 0};
+    while (c.r >= nr) {
+        c.r -= nr;
+        c.i++;
+    }
+    g1_occ_block(a, w, c.i, c.k, c.blk);
+    c.s = g1_shard_of_seg<ONE>(a, sht, w.S_first + c.k);
+    c.nxt = !ONE && c.s + 1 < a.nshards ? sht[c.s + 1].sbeg : 0x7fffffff;
+    return c;
+}
+
+// Occurrences run through the blocks of the first segment from tr0 / 8, then through every
+// block 0 .. nbpc - 1 of each next segment, so the block steps like a mixed-radix counter;
+// shards hold consecutive segments, so the shard index only grows.
+template <bool ONE>
+G1_HD void g1_task_next(const G1Group& a, const G1Shard* sht, const G1Range& w, G1Task& c, int nr, G1TaskStep st)
+{
+    c.t += G1_NW;
+    int d = st.q;
+    c.r += st.rm;
+    if (c.r >= nr) {
+        c.r -= nr;
+        d++;
+    }
+    c.i += d;
+    c.blk += d;
+    while (c.blk >= w.nbpc) {
+        c.blk -= w.nbpc;
+        c.k++;
+    }
+    if constexpr (!ONE)
+        while (w.S_first + c.k >= c.nxt) {
+            c.s++;
+            c.nxt = c.s + 1 < a.nshards ? sht[c.s + 1].sbeg : 0x7fffffff;
+        }
+}
+
 // Workgroups g_lo .. g_hi whose ranges hold units of segment S (g_hi > g_lo: split).
 template <bool ONE>
 G1_HD void g1_contributors(const G1Group& a, const G1Shard* sht, int S, int& g_lo, int& g_hi)
@@ -311,24 +373,40 @@ G1_HD bool g1_run_meets(const G1Run& run, int b, int e)
 }
 
 // nr = activation rows the tables hold (1, or the call's rows for the multi-row template).
-// red[nseg + G1_NW - 1][nr][128] fp32 partial rows | act[nocc][8][nr][16] duplicated fp16
-// activations (u32 words) | zero[16] (the A operand of the lanes whose k-block is not theirs).
+// red[nseg + G1_NW - 1][nr][128] fp32 partial rows | act: the duplicated fp16 activations
+// (u32 words) | zero (the A operand of the lanes whose k-block is not theirs).
 // Wave ww's partial rows of the range's k-th segment are red[k + ww]: a wave's run is one
 // contiguous piece of the range and the runs are in wave order, so two (segment, wave) pairs
 // that both hold units never share k + ww (if wave ww meets segment k + 1, wave ww + 1 starts
 // at or after it and cannot meet segment k).  Only such pairs are written and read.
+//
+// A unit's A operand is four 16-byte LDS reads per lane (chunks c = 0..3 of its row's 16
+// words), the same immediate offsets for every lane.  One row: act[nocc][8][4 c][4] (every
+// A-carrying lane reads the same chunk, a broadcast), then zero[16].  Several rows:
+// act[nocc][8][4 c][G1_ROWS slots][4] -- chunk c of rows 0..3 is 16 consecutive words, one
+// bank each, where row-major rows 64 bytes apart share banks -- then zero, its four chunks
+// 16 words apart (measured on MI355X, gate/up at four rows: 41.4 -> 40.5-41.0 us per call
+// against row-major rows; moving zero off the banks of the act chunks read beside it
+// measured no faster, with one row or several).  Slots of rows >= nr are not written (their
+// lanes read row nr - 1).
 struct G1Lds {
     int act;                   // u32 offset of act
     int zero;                  // u32 offset of zero
     int words;                 // u32 words in all
 };
 
+// u32 words per table entry (occurrence, tile row), bytes between a lane's four A chunks,
+// and zero words the kernel clears.
+G1_HD constexpr int g1_entry_words(int nr) { return nr == 1 ? 16 : 16 * G1_ROWS; }
+G1_HD constexpr int g1_a_chunk(int nr) { return nr == 1 ? 16 : 64; }
+G1_HD constexpr int g1_zero_words(int nr) { return nr == 1 ? 16 : 3 * 16 + 4; }
+
 G1_HD G1Lds g1_lds_layout(int nseg, int nocc, int nr)
 {
     G1Lds l;
     l.act = (nseg + G1_NW - 1) * nr * 128;
-    l.zero = l.act + nocc * nr * 128;
-    l.words = l.zero + 16;
+    l.zero = l.act + nocc * 8 * g1_entry_words(nr);
+    l.words = l.zero + g1_zero_words(nr);
     return l;
 }
 
@@ -339,16 +417,18 @@ G1_HD int g1_red_row(int k, int ww, int nr, int r)
 }
 
 // u32 word (of act) where lane l stores activation row r's outputs 2l, 2l + 1 of occurrence
-// i as two duplicated fp16 pairs: act[i][tile row l / 8][r][m][t] holds row 2m +
-// {0, 1, 8, 9}[t] of the tile row, lane l's rows are m = l % 4, t = 2 ((l % 8) / 4), t + 1.
+// i as two duplicated fp16 pairs: chunk c = l % 4 of tile row l / 8 holds rows 2c +
+// {0, 1, 8, 9}[t] of the tile row, lane l's are t = 2 ((l % 8) / 4), t + 1.
 G1_HD int g1_act_word(int i, int lane, int nr, int r)
 {
-    return ((i * 8 + (lane >> 3)) * nr + r) * 16 + 4 * (lane & 3) + 2 * ((lane >> 2) & 1);
+    const int c = lane & 3, t = 2 * ((lane >> 2) & 1);
+    const int e = (i * 8 + (lane >> 3)) * g1_entry_words(nr);
+    return nr == 1 ? e + 4 * c + t : e + (c * G1_ROWS + r) * 4 + t;
 }
 
 // The lane's A operand: row i = lane % 16 in k-block lane / 16, which carries activation row
-// i / 4 when i % 4 is that k-block (asel = 1) and zeros otherwise (asel = 0).  Its 64 LDS
-// bytes for a unit whose table entry starts at byte e are at e * asel + aoff.
+// i / 4 when i % 4 is that k-block (asel = 1) and zeros otherwise (asel = 0).  Its chunk c
+// for a unit whose table entry starts at byte e is at e * asel + aoff + c * g1_a_chunk(nr).
 G1_HD uint32_t g1_asel(int lane)
 {
     return ((lane & 15) & 3) == (lane >> 4) ? 1u : 0u;
@@ -357,13 +437,13 @@ G1_HD uint32_t g1_asel(int lane)
 G1_HD uint32_t g1_aoff(int lane, int nr, const G1Lds& l)
 {
     const int rr = (lane & 15) >> 2;
-    return g1_asel(lane) ? (uint32_t)(4 * l.act + (rr < nr - 1 ? rr : nr - 1) * 64) : (uint32_t)(4 * l.zero);
+    return g1_asel(lane) ? (uint32_t)(4 * l.act + (rr < nr - 1 ? rr : nr - 1) * 16) : (uint32_t)(4 * l.zero);
 }
 
 // Byte offset (relative to act) of the table entry of occurrence occ, tile row tr.
 G1_HD uint32_t g1_a_entry(int occ, int tr, int nr)
 {
-    return (uint32_t)((occ * 8 + (tr & 7)) * nr) * 64u;
+    return (uint32_t)((occ * 8 + (tr & 7)) * g1_entry_words(nr)) * 4u;
 }
 
 // Where lane l's accumulators land in a partial row: activation row yrow, outputs
@@ -415,7 +495,7 @@ inline size_t g1_lds_bytes(int U, int G, int ntr, int nr)
     const int L = (U + G - 1) / G;
     const int nseg = (L - 1 + ntr - 1) / ntr + 1;
     const int nocc = (L + 6) / 8 + 1;
-    return (size_t)(nseg + G1_NW - 1) * nr * 128 * sizeof(float) + (size_t)nocc * nr * 128 * sizeof(uint32_t) + 64;
+    return (size_t)g1_lds_layout(nseg, nocc, nr).words * sizeof(uint32_t);
 }
 
 // Row-count template of a call: one activation row, or up to four (G1_ROWS).

@@ -131,17 +131,27 @@ void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G
     auto trellis_words = [&](int gi) { return (long)(W.sh[gi].ic / 16) * (W.sh[gi].oc / 16) * 8 * K; };
 
     // ---- zero operand
-    for (int t = 0; t < 16; t++)
+    for (int t = 0; t < g1_zero_words(nr); t++)
         if (ll.zero + t >= ll.words) fail("zero word out of LDS");
+    if (g1_zero_words(nr) > 64 * G1_NW) fail("more zero words than threads clear them");
+    std::vector<char> act_written((size_t)(ll.zero - ll.act), 0);
 
     // ---- activation table: tag of each occurrence (segment k, block); each (occurrence, row)
     // transformed once
     std::vector<int> occ_k(w.nocc, -1), occ_blk(w.nocc, -1), occ_rows(w.nocc, 0);
+    // (the kernel's task cursor, checked against the division form of each task)
+    const G1TaskStep tst = g1_task_step(nr);
+    if (tst.q * nr + tst.rm != G1_NW || tst.rm < 0 || tst.rm >= nr) fail("task step %d %d for %d rows", tst.q, tst.rm, nr);
     for (int wave = 0; wave < G1_NW; wave++)
-        for (int t = wave; t < w.nocc * nr; t += G1_NW) {
-            const int i = R == 1 ? t : t / nr, r = t - i * nr;
+        for (G1Task tk = g1_task_first<ONE>(a, sht, w, wave, nr); tk.t < w.nocc * nr;
+             g1_task_next<ONE>(a, sht, w, tk, nr, tst)) {
+            const int t = tk.t, i = tk.i, r = tk.r;
+            if (i != t / nr || r != t % nr) fail("task %d: cursor (%d, %d) for %d rows", t, i, r, nr);
             int k, blk;
             g1_occ_block(a, w, i, k, blk);
+            if (tk.k != k || tk.blk != blk)
+                fail("task %d: cursor at (segment %d, block %d), occurrence %d is (%d, %d)", t, tk.k, tk.blk, i, k, blk);
+            if (tk.s != g1_shard_of_seg<ONE>(a, sht, w.S_first + k)) fail("task %d: cursor shard %d", t, tk.s);
             if (k < 0 || k >= w.nseg) fail("occurrence %d: segment %d of %d", i, k, w.nseg);
             if (blk < 0 || blk >= ntr / 8) fail("occurrence %d: block %d of %d", i, blk, ntr / 8);
             if (occ_k[i] >= 0 && (occ_k[i] != k || occ_blk[i] != blk)) fail("occurrence %d: two blocks", i);
@@ -160,6 +170,8 @@ void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G
                 if (g1_x_elem(a, r, blk) / ic != r) fail("activation row %d reads row %ld", r, g1_x_elem(a, r, blk) / ic);
                 const int aw = g1_act_word(i, lane, nr, r);
                 if (aw < 0 || aw + 2 > ll.zero - ll.act) fail("act store outside act (word %d)", aw);
+                if (aw % 2) fail("act store at odd word %d (an 8-byte store)", aw);
+                if (act_written[aw]++ || act_written[aw + 1]++) fail("act word %d stored twice", aw);
             }
         }
     for (int i = 0; i < w.nocc; i++)
@@ -227,17 +239,26 @@ void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G
                     const uint32_t ent = g1_a_entry(occ, cu.tr, nr);
                     for (int lane = 0; lane < 64; lane++) {
                         const uint32_t asel = g1_asel(lane), aoff = g1_aoff(lane, nr, ll);
-                        const uint32_t byte = ent * asel + aoff;
-                        if (asel) {
-                            if (byte < 4u * ll.act || byte + 64 > 4u * ll.zero) fail("A read outside act");
-                            // it must be the table row (occurrence, tile row, activation row)
-                            const uint32_t rel = (byte - 4u * ll.act) / 64;
-                            const int want_r = std::min((lane & 15) >> 2, nr - 1);
-                            if (rel != (uint32_t)((occ * 8 + (cu.tr & 7)) * nr + want_r)) fail("A read of a wrong table row");
-                        } else if (byte != 4u * ll.zero) {
-                            fail("zero-operand lane reads byte %u, not the zero words", byte);
+                        const int want_r = std::min((lane & 15) >> 2, nr - 1);
+                        for (int c = 0; c < 4; c++) {
+                            // chunk c: 16 bytes at the kernel's immediate offset c * g1_a_chunk
+                            const uint32_t byte = ent * asel + aoff + c * g1_a_chunk(nr);
+                            if (byte % 16) fail("A chunk at byte %u is not 16-byte aligned", byte);
+                            if (byte + 16 > 4u * ll.words) fail("A read beyond the LDS layout");
+                            if (asel) {
+                                // the 4 words the table store of (occurrence, tile row, activation
+                                // row, chunk c) wrote: lanes 8 (tr % 8) + c and + 4 of that store
+                                const int wa = g1_act_word(occ, 8 * (cu.tr & 7) + c, nr, want_r);
+                                const int wb = g1_act_word(occ, 8 * (cu.tr & 7) + c + 4, nr, want_r);
+                                if (byte != 4u * (ll.act + wa) || wb != wa + 2)
+                                    fail("A chunk %d of lane %d reads byte %u, table word %d", c, lane, byte, ll.act + wa);
+                                if (byte + 16 > 4u * ll.zero) fail("A read outside act");
+                            } else {
+                                const uint32_t z = byte - 4u * ll.zero;
+                                if (byte < 4u * ll.zero || z + 16 > 4u * g1_zero_words(nr))
+                                    fail("zero-operand lane %d chunk %d reads byte %u, not the cleared words", lane, c, byte);
+                            }
                         }
-                        if (byte + 64 > 4u * ll.words) fail("A read beyond the LDS layout");
                     }
                     W.lds_reads++;
                     if (j + d + 1 < n) {

@@ -126,6 +126,15 @@ def test_gemv1_many_shards(rl):
     assert st[0] >= 3
 
 
+@pytest.mark.parametrize("rows", [1, 3, 4])
+def test_gemv1_table_tasks_cross_several_shards(rl, rows):
+    # 128 inputs (one block per column group) and nine column groups per shard on one CU: each
+    # workgroup's range spans ~18 segments, and a wave's activation-table tasks step over
+    # 8 / rows of them at a time, crossing two shard boundaries in one wave's walk
+    ok(gemv1(rl, rows, 128, [1152] * 8, [2, 3, 4, 5, 6, 7, 8, 1], [0, 1] * 4, cus=1), f"rows={rows}")
+    ok(gemv1(rl, rows, 256, [384, 128, 640, 128, 256, 128, 1152, 128], [4] * 8, cus=1), f"rows={rows} ragged")
+
+
 def test_gemv1_random_shapes(rl):
     rnd = random.Random(20260)
     for case in range(300):
