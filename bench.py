@@ -24,7 +24,8 @@ calibration workload).
 reconstruct_weight Hadamard/sign algebra in fp32 torch, F.linear), timed on this host's
 cores on one step of the same workload.
 `tok_s_equiv` / `stack` = config 4 measured: the whole 64-layer linear stack + lm_head +
-embedding gather of one batch-1 token as one HIP graph, replayed (attention excluded).
+its argmax epilogue + the embedding gather of the argmax token, one batch-1 greedy token as
+one HIP graph, replayed (attention excluded).
 
     python bench.py --workload config2   # grouped qkv / gate_up GEMVs at batch 1, 4, 16
     python bench.py --workload config3   # M=2048 prefill GEMM (TFLOP/s, MFMA share) + reconstruct
@@ -314,18 +315,31 @@ def stack_bench(tokens: int = 20) -> dict:
             _native.gemv_grouped(gate_cols, [L["down"]], out=y_h)
             h = y_h
         _native.gemv_grouped(h, [head], out=logits)
+        ids.copy_(_native.argmax(logits))       # greedy: the next token's embedding row
 
     graph, side = _graph(dev, token)
     sec = _time_graph(graph, side, tokens)
     finite = bool(torch.isfinite(logits).all().item())
     rms = float(logits.float().pow(2).mean().sqrt().item())
     del graph
+    # the argmax / top-k epilogue alone on the same logits: 20 calls per graph, so a replay's
+    # launch cost is spread over them
+    epilogue = {}
+    for name, k in (("argmax", 1), ("top64", 64)):
+        def calls(k=k):
+            for _ in range(20):
+                _native.topk(logits, k)
+        g2, side2 = _graph(dev, calls)
+        epilogue[name] = round(_time_graph(g2, side2, 20) * 1e6 / 20, 2)
+        del g2
     return {"tok_s": round(1.0 / sec, 2), "ms_per_token": round(sec * 1e3, 4), "bytes_per_token": nbytes,
             "GB/s": round(nbytes / sec / 1e9, 1), "frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4),
             "tokens": tokens, "logits_finite": finite, "logits_rms": round(rms, 4),
-            "what": "config4 measured: 64-layer Qwen-27B-shaped linear stack + K=6 lm_head + int8 embedding "
-                    "gather, batch 1, each projection chained on the previous output, one HIP-graph-launched "
-                    "token replayed; attention/KV/norms/activation excluded"}
+            "epilogue_us": epilogue,
+            "what": "config4 measured: 64-layer Qwen-27B-shaped linear stack + K=6 lm_head + argmax epilogue "
+                    "+ int8 embedding gather of the argmax token, batch 1, each projection chained on the "
+                    "previous output, one HIP-graph-launched token replayed; attention/KV/norms/activation "
+                    "excluded"}
 
 
 def config2_bench(reps: int) -> dict:

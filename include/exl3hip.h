@@ -175,6 +175,26 @@ int exl3_gemm_grouped(const void* A, const exl3_shard_t* shards, int nshards, vo
 int exl3_embed_int8_gather(const void* table, const void* scales, int scale_dtype, const void* ids,
                            void* out, long n_ids, int vocab, int dim, void* stream);
 
+/*
+ * Argmax / top-k epilogue of the output head: the k largest entries of each row of an fp16
+ * matrix (the logits the K=6 lm_head's exl3_gemv writes), largest first, equal values by
+ * smaller column; every NaN ranks above +inf (torch.argmax's order), -0 equals +0.  k = 1 is
+ * the argmax of greedy decoding.  x (rows, ld) fp16, 16-byte aligned, ld % 8 == 0,
+ * n <= ld columns used (each row may be read up to column ceil(n / 8) * 8 - 1);
+ * 1 <= k <= EXL3_TOPK_MAX_K, k <= n <= EXL3_TOPK_MAX_N.  values (rows, k)
+ * fp16 (the entries' own bits), indices (rows, k) int64.  workspace >=
+ * exl3_topk_workspace_bytes(rows, n, k) bytes, 8-byte aligned.  Two kernels on the stream;
+ * nothing allocated.
+ * No counterpart in the reference: its lm_head is an ordinary EXL3 linear
+ * [orcasaq2/config.py:128-132] whose logits vLLM's sampler reduces; this is that reduction on
+ * the GEMV's stream.
+ */
+#define EXL3_TOPK_MAX_K 64
+#define EXL3_TOPK_MAX_N (1 << 19)
+size_t exl3_topk_workspace_bytes(int rows, int n, int k);
+int exl3_topk(const void* x, int rows, int n, long ld, int k, void* values, void* indices, void* workspace,
+              size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -13,6 +13,9 @@ fp64, restating the reference:
   * fused order y = H(H(x * suh) W_q) * svh, fp16 A_had .... orcasaq2/ops.py:44-59
   * activations cast to fp16, concat of shards ............ orcasaq2/config.py:232-245
   * int8 embedding: q[ids] * s[ids] ........................ orcasaq2/heads.py:61-67
+  * top-k / argmax of the head's logits ..................... no reference counterpart (vLLM's
+    sampler reduces the logits of orcasaq2/config.py:128-132); restates torch.argmax's order
+    (first maximal column, NaN above every number, -0 == +0) with ties by smaller column
 """
 from __future__ import annotations
 
@@ -206,3 +209,26 @@ def embed_int8_ref(q, s, ids) -> np.ndarray:
     s = np.asarray(s).reshape(-1, 1)
     ids = np.asarray(ids).reshape(-1)
     return (q[ids].astype(np.float32) * s[ids].astype(np.float32)).astype(s.dtype)
+
+
+def fp16_order_key(x) -> np.ndarray:
+    """Unsigned order key of fp16 values: larger for larger values, -0 and +0 alike, every
+    NaN above +inf (torch.argmax's order)."""
+    h = np.asarray(x, np.float16).view(np.uint16).astype(np.int64)
+    mag = h & 0x7FFF
+    key = np.where(h & 0x8000, (~h) & 0xFFFF, h | 0x8000)
+    key = np.where(mag == 0, 0x8000, key)
+    return np.where(mag > 0x7C00, 0xFFFF, key)
+
+
+def topk_rows(x, k: int):
+    """The k largest entries of each row of fp16 x (rows, n): values (rows, k) fp16 (the
+    entries' own bits) largest first, equal values by smaller column, and their columns
+    (rows, k) int64."""
+    x = np.asarray(x, np.float16).reshape(-1, np.shape(x)[-1])
+    key = fp16_order_key(x)
+    cols = np.arange(x.shape[1])
+    idx = np.empty((x.shape[0], k), np.int64)
+    for r in range(x.shape[0]):
+        idx[r] = np.lexsort((cols, -key[r]))[:k]     # primary: key descending; then column
+    return np.take_along_axis(x, idx, axis=1), idx

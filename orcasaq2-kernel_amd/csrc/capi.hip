@@ -56,7 +56,7 @@ extern "C" {
 
 const char* exl3_last_error(void) { return g_err; }
 
-int exl3_abi_version(void) { return 5; }
+int exl3_abi_version(void) { return 6; }
 
 int exl3_stream_capture_id(void* stream, unsigned long long* id)
 {
@@ -243,6 +243,30 @@ int exl3_embed_int8_gather(const void* table, const void* scales, int scale_dtyp
         return set_error(EXL3_ERR_ARG, "exl3_embed_int8_gather: misaligned pointer");
     return embed_dispatch(static_cast<const int8_t*>(table), scales, scale_dtype, static_cast<const int64_t*>(ids),
                           out, n_ids, vocab, dim, static_cast<hipStream_t>(stream));
+}
+
+size_t exl3_topk_workspace_bytes(int rows, int n, int k) { return topk_workspace_bytes(rows, n, k); }
+
+int exl3_topk(const void* x, int rows, int n, long ld, int k, void* values, void* indices, void* workspace,
+              size_t workspace_bytes, void* stream)
+{
+    g_err[0] = 0;
+    if (rows < 0 || rows > 65535)
+        return set_error(EXL3_ERR_ARG, "exl3_topk: rows=%d is not in 0..65535", rows);
+    if (k < 1 || k > EXL3_TOPK_MAX_K || n < k || n > EXL3_TOPK_MAX_N)
+        return set_error(EXL3_ERR_ARG, "exl3_topk: k=%d n=%d (need 1 <= k <= %d, k <= n <= %d)", k, n,
+                         EXL3_TOPK_MAX_K, EXL3_TOPK_MAX_N);
+    if (ld < n || ld % 8)
+        return set_error(EXL3_ERR_ARG, "exl3_topk: ld=%ld (need ld >= n=%d, ld %% 8 == 0)", ld, n);
+    if (rows == 0) return EXL3_OK;
+    if (!x || !values || !indices || !workspace) return set_error(EXL3_ERR_ARG, "exl3_topk: null pointer");
+    if (!aligned(x, 16) || !aligned(values, 2) || !aligned(indices, 8) || !aligned(workspace, 8))
+        return set_error(EXL3_ERR_ARG, "exl3_topk: misaligned pointer (x 16, values 2, indices 8, workspace 8 bytes)");
+    const size_t need = topk_workspace_bytes(rows, n, k);
+    if (workspace_bytes < need)
+        return set_error(EXL3_ERR_WORKSPACE, "exl3_topk: workspace %zu bytes < %zu needed", workspace_bytes, need);
+    return topk_dispatch(static_cast<const uint16_t*>(x), rows, n, ld, k, static_cast<uint16_t*>(values),
+                         static_cast<int64_t*>(indices), workspace, static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

@@ -57,4 +57,10 @@ int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, c
 int embed_dispatch(const int8_t* table, const void* scales, int scale_dtype, const int64_t* ids,
                    void* out, long n_ids, int vocab, int dim, hipStream_t stream);
 
+constexpr int TK_MAX_K = EXL3_TOPK_MAX_K;
+constexpr int TK_MAX_N = EXL3_TOPK_MAX_N;
+size_t topk_workspace_bytes(int rows, int n, int k);
+int topk_dispatch(const uint16_t* x, int rows, int n, long ld, int k, uint16_t* values, int64_t* idx,
+                  void* workspace, hipStream_t stream);
+
 }  // namespace exl3

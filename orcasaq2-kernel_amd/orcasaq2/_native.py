@@ -16,11 +16,13 @@ import torch
 
 LIB_NAME = "libexl3hip.so"
 LIB_PATH = os.environ.get("ORCASAQ2_LIB", os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME))
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 CB_3INST, CB_MCG, CB_MUL1 = 0, 1, 2
 GEMV_MAX_ROWS = 16
 MAX_SHARDS = 64
+TOPK_MAX_K = 64
+TOPK_MAX_N = 1 << 19
 
 _lib = None
 _lock = threading.Lock()
@@ -66,6 +68,10 @@ _SIGS = {
     "exl3_embed_int8_gather": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                               ctypes.c_void_p, ctypes.c_void_p, ctypes.c_long,
                                               ctypes.c_int, ctypes.c_int, ctypes.c_void_p]),
+    "exl3_topk_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "exl3_topk": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_long, ctypes.c_int,
+                                 ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                 ctypes.c_void_p]),
 }
 
 EXPORTED = tuple(_SIGS)
@@ -382,3 +388,45 @@ def embed_int8(table: torch.Tensor, scales: torch.Tensor, ids: torch.Tensor) -> 
     _check(lib().exl3_embed_int8_gather(_ptr(table), _ptr(scales), _SCALE_DTYPES[scales.dtype], _ptr(idx),
                                         _ptr(out), idx.numel(), vocab, dim, _stream(dev)), fn)
     return out.reshape(*ids.shape, dim)
+
+
+def topk(x: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """The k largest entries of each row of fp16 x (..., n), e.g. the output head's logits:
+    values (..., k) fp16, largest first, equal values by smaller column, every NaN above
+    +inf and -0 equal to +0, and their columns (..., k) int64 (exl3_topk).  k = 1 is greedy
+    decoding's argmax.  A row layout the kernel cannot read (column stride != 1, row stride
+    not a multiple of 8, base not 16-byte aligned) is first copied to one it can."""
+    fn = "exl3_topk"
+    dev = _need_gpu(fn, x)
+    _need(x.dtype == torch.float16, fn, f"x must be fp16, got {x.dtype}")
+    _need(x.dim() >= 1 and x.shape[-1] >= 1, fn, f"x must have a non-empty last dim, got {tuple(x.shape)}")
+    n = x.shape[-1]
+    _need(1 <= k <= TOPK_MAX_K and k <= n <= TOPK_MAX_N, fn,
+          f"k={k} n={n} (need 1 <= k <= {TOPK_MAX_K}, k <= n <= {TOPK_MAX_N})")
+    x2 = x.reshape(-1, n)
+    rows = x2.shape[0]
+    _need(rows <= 65535, fn, f"{rows} rows (at most 65535)")
+    ld = x2.stride(0) if rows > 1 else (n + 7) // 8 * 8
+    readable = x2.stride(-1) == 1 and ld % 8 == 0 and ld >= n and x2.data_ptr() % 16 == 0
+    if readable:
+        # the kernel may read each row up to the next multiple of 8 columns, which must lie
+        # inside x's storage for the last row too
+        end = x2.storage_offset() + (rows - 1) * ld + (n + 7) // 8 * 8
+        readable = end <= x2.untyped_storage().nbytes() // 2
+    if not readable:
+        ld = (n + 7) // 8 * 8
+        xp = torch.empty((rows, ld), dtype=torch.float16, device=dev)
+        xp[:, :n].copy_(x2)
+        x2 = xp
+    values = torch.empty((rows, k), dtype=torch.float16, device=dev)
+    idx = torch.empty((rows, k), dtype=torch.int64, device=dev)
+    L = lib()
+    ws = workspace(dev, L.exl3_topk_workspace_bytes(rows, n, k))
+    _check(L.exl3_topk(_ptr(x2), rows, n, ld, k, _ptr(values), _ptr(idx), _ptr(ws), ws.numel(), _stream(dev)), fn)
+    return values.reshape(*x.shape[:-1], k), idx.reshape(*x.shape[:-1], k)
+
+
+def argmax(x: torch.Tensor) -> torch.Tensor:
+    """Column of each row's largest entry of fp16 x (..., n) (the first one of equal maxima,
+    as torch.argmax): topk with k = 1."""
+    return topk(x, 1)[1][..., 0]

@@ -311,6 +311,13 @@ class Exl3LinearMethod(LinearMethodBase):
         if layer.exl3_shards is None:
             out = torch.nn.functional.linear(x, layer.exl3_dense.to(x.dtype))
             return out + bias if bias is not None else out
+        out = self.apply_fp16(layer, x).to(x.dtype)
+        return out + bias if bias is not None else out
+
+    def apply_fp16(self, layer, x: torch.Tensor) -> torch.Tensor:
+        """The shards' fp16 outputs of apply, before the cast to x.dtype and the bias."""
+        if layer.exl3_shards is None:
+            raise RuntimeError(f"{self.prefix}: a dense fallback layer has no fp16 EXL3 output")
         rows = x.numel() // x.shape[-1]
         xf = x.reshape(rows, x.shape[-1]).half()
         if not xf.is_contiguous():
@@ -326,5 +333,4 @@ class Exl3LinearMethod(LinearMethodBase):
             outs = [torch.ops.orcasaq2.shard_gemm(xf, s.trellis, s.suh, s.svh, s.oc, float(s.K), s.mcg, s.mul1)
                     for s in shards]
             out = outs[0] if len(outs) == 1 else torch.cat(outs, dim=-1)
-        out = out.to(x.dtype).reshape(*x.shape[:-1], out.shape[-1])
-        return out + bias if bias is not None else out
+        return out.reshape(*x.shape[:-1], out.shape[-1])

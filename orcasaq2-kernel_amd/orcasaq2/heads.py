@@ -2,6 +2,8 @@
 
 * `lm_head` needs nothing here: when a pack quantizes it (`head_bits`) it is an ordinary
   EXL3 tensor, and Exl3Config.get_quant_method gives ParallelLMHead the linear method.
+  `lm_head_topk` adds the argmax / top-k epilogue (exl3_topk) behind it for greedy and
+  top-k decoding, on the fp16 logits the GEMV writes.
 * `embed_tokens` arrives either as int8 rows with one scale per row or as a plain table.
   The int8 table stays int8 in device memory: a lookup gathers the requested rows and
   scales only those, in the HIP library (exl3_embed_int8_gather); a tied head dequantizes
@@ -63,3 +65,19 @@ class Exl3EmbeddingMethod(QuantizeMethodBase):
             table = layer.exl3_embed
         out = torch.nn.functional.linear(x, table.to(x.dtype))
         return out if bias is None else out + bias
+
+
+def lm_head_topk(layer, x: torch.Tensor, k: int = 1) -> tuple[torch.Tensor, torch.Tensor]:
+    """The output head and its top-k epilogue: the quantized lm_head's fp16 logits for
+    hidden states x (..., hidden) (its EXL3 linear method, reference orcasaq2/config.py:
+    128-132), then each row's k largest (values fp16 and columns int64, largest first,
+    equal logits by smaller column; k = 1 is greedy decoding's argmax), both on the current
+    stream.  A head with a bias adds it to the fp16 logits first."""
+    method = getattr(layer, "quant_method", None)
+    if not hasattr(method, "apply_fp16"):
+        raise RuntimeError("lm_head_topk: the layer does not use the EXL3 linear method")
+    logits = method.apply_fp16(layer, x)
+    bias = getattr(layer, "bias", None)
+    if bias is not None:
+        logits = logits + bias.to(torch.float16)
+    return _native.topk(logits, k)

@@ -125,3 +125,26 @@ def test_wrappers_refuse_cpu_tensors(native):
         native.gemv(x, t, torch.ones(128, dtype=torch.float16), torch.ones(128, dtype=torch.float16), 4, 0)
     with pytest.raises(RuntimeError, match="GPU"):
         native.reconstruct(t, 4, 0)
+
+
+def test_topk_rejects_bad_arguments_on_host(native):
+    L = native.lib()
+    fake, ws = P(0x10000), P(0x100000)
+    big = 1 << 30
+
+    def call(rows=2, n=4096, ld=4096, k=8, x=fake, wsb=big, values=fake, indices=fake):
+        return L.exl3_topk(x, rows, n, ld, k, values, indices, ws, wsb, None)
+
+    assert call(k=0) == 1 and "k=0" in _err(native)
+    assert call(k=65) == 1 and "k=65" in _err(native)
+    assert call(n=7, ld=8) == 1                                  # k > n
+    assert call(n=(1 << 19) + 8, ld=(1 << 19) + 8) == 1           # n beyond the bound
+    assert call(ld=4100) == 1 and "ld=4100" in _err(native)      # ld % 8
+    assert call(ld=4088) == 1                                    # ld < n
+    assert call(rows=-1) == 1 and call(rows=70000) == 1
+    assert call(x=P(0x10008)) == 1 and "misaligned" in _err(native)
+    assert call(indices=P(0x10004)) == 1
+    assert call(wsb=8) == 3 and "workspace" in _err(native)
+    assert L.exl3_topk_workspace_bytes(2, 4096, 8) == 2 * 1 * 8 * 8
+    assert L.exl3_topk_workspace_bytes(1, 151936, 64) == 38 * 64 * 8     # 4096-column chunks
+    assert call(rows=0) == 0                                     # nothing to do, nothing enqueued

@@ -204,3 +204,64 @@ def test_embed_int8_reference_semantics(oracle):
     want = (torch.from_numpy(q)[torch.from_numpy(ids)].to(torch.float16)
             * torch.from_numpy(s)[torch.from_numpy(ids)]).numpy()
     assert np.array_equal(oracle.embed_int8_ref(q, s, ids).view(np.uint16), want.view(np.uint16))
+
+
+# ---------------------------------------------------------------- top-k / argmax of the head's logits
+
+def _brute_topk(row, k):
+    # total order written out case by case: NaN first (ties by column), then by value
+    # (-0 == +0), ties by column
+    def rank(i):
+        v = float(row[i])
+        return (0, 0.0, i) if np.isnan(v) else (1, -v, i)
+    order = sorted(range(len(row)), key=rank)[:k]
+    return np.array(order, np.int64)
+
+
+def test_fp16_order_key_is_monotone_over_every_fp16(oracle):
+    h = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    v = h.view(np.float16)
+    key = oracle.fp16_order_key(v)
+    finite = ~np.isnan(v)
+    f = v[finite].astype(np.float64)
+    kf = key[finite]
+    o = np.argsort(f, kind="stable")
+    assert np.all(np.diff(kf[o]) >= 0)                      # value order kept
+    assert np.all((np.diff(f[o]) == 0) == (np.diff(kf[o]) == 0))   # equal keys iff equal values
+    assert np.all(key[~finite] == 0xFFFF) and kf.max() == 0xFC00 and kf.min() == 0x03FF
+    assert key[np.float16(0.0).view(np.uint16)] == key[np.float16(-0.0).view(np.uint16)] == 0x8000
+
+
+def test_topk_oracle_matches_torch_argmax_and_topk(oracle):
+    rng = np.random.default_rng(5)
+    # heavy ties: values drawn from a small set, plus +-0, +-inf and NaN in some rows
+    x = rng.choice(np.array([-3, -1, -0.0, 0.0, 0.5, 2, 7], np.float16), size=(40, 300))
+    x[3, 17] = np.inf
+    x[5, [9, 200]] = np.nan
+    x[6, :] = -np.inf
+    x[7, 150] = -np.inf
+    xt = torch.from_numpy(x)
+    v1, i1 = oracle.topk_rows(x, 1)
+    assert np.array_equal(i1[:, 0], torch.argmax(xt, dim=1).numpy())
+    assert np.array_equal(i1[:, 0], torch.argmax(xt.float(), dim=1).numpy())
+    # distinct values: torch.topk's order is the oracle's
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    finite = bits[~np.isnan(bits.view(np.float16)) & (bits != 0x8000)]          # distinct values
+    y = rng.choice(finite, size=4000, replace=False).view(np.float16).reshape(4, 1000)
+    for k in (1, 5, 64):
+        vk, ik = oracle.topk_rows(y, k)
+        tv, ti = torch.topk(torch.from_numpy(y).float(), k, dim=1, sorted=True)
+        assert np.array_equal(vk.astype(np.float32), tv.numpy()) and np.array_equal(ik, ti.numpy())
+
+
+def test_topk_oracle_matches_brute_force_on_ties_and_special_values(oracle):
+    rng = np.random.default_rng(9)
+    pool = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0, 1.0, -1.0, 65504, -65504, 6e-8, -6e-8], np.float16)
+    for case in range(200):
+        n = int(rng.integers(1, 40))
+        row = rng.choice(pool, size=n)
+        k = int(rng.integers(1, n + 1))
+        v, i = oracle.topk_rows(row[None, :], k)
+        want = _brute_topk(row, k)
+        assert np.array_equal(i[0], want), (case, row, k)
+        assert np.array_equal(v[0].view(np.uint16), row[want].view(np.uint16))   # the entries' own bits
