@@ -382,13 +382,15 @@ G1_HD bool g1_run_meets(const G1Run& run, int b, int e)
 //
 // A unit's A operand is four 16-byte LDS reads per lane (chunks c = 0..3 of its row's 16
 // words), the same immediate offsets for every lane.  One row: act[nocc][8][4 c][4] (every
-// A-carrying lane reads the same chunk, a broadcast), then zero[16].  Several rows:
-// act[nocc][8][4 c][G1_ROWS slots][4] -- chunk c of rows 0..3 is 16 consecutive words, one
-// bank each, where row-major rows 64 bytes apart share banks -- then zero, its four chunks
-// 16 words apart (measured on MI355X, gate/up at four rows: 41.4 -> 40.5-41.0 us per call
-// against row-major rows; moving zero off the banks of the act chunks read beside it
-// measured no faster, with one row or several).  Slots of rows >= nr are not written (their
-// lanes read row nr - 1).
+// A-carrying lane reads the same chunk, a broadcast) and zero[16], starting 8 words past a
+// multiple of 16 so that its chunk c never shares a bank with the act chunk c read beside
+// it.  Several rows: act[nocc][8][4 c][G1_ROWS slots][4] (chunk c of rows 0..3 is 16
+// consecutive words) and zero, its four chunks 16 words apart, starting 16 words past a
+// multiple of 32: the zero and act chunks of one read fall in distinct banks for 32 or 64
+// banks of 4 bytes.  Measured on MI355X (config 2, SQ_LDS_BANK_CONFLICT per dispatch): one
+// row 348,160 -> 0, four rows 2,047,968 -> 655,328 (the table stores and partial rows keep
+// the rest), with no change in busy cycles -- the conflicts were off the critical path.
+// Slots of rows >= nr are not written (their lanes read row nr - 1).
 struct G1Lds {
     int act;                   // u32 offset of act
     int zero;                  // u32 offset of zero
@@ -405,7 +407,7 @@ G1_HD G1Lds g1_lds_layout(int nseg, int nocc, int nr)
 {
     G1Lds l;
     l.act = (nseg + G1_NW - 1) * nr * 128;
-    l.zero = l.act + nocc * 8 * g1_entry_words(nr);
+    l.zero = l.act + nocc * 8 * g1_entry_words(nr) + (nr == 1 ? 8 : 16);
     l.words = l.zero + g1_zero_words(nr);
     return l;
 }
