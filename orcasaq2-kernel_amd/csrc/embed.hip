@@ -27,33 +27,48 @@ __device__ __forceinline__ uint16_t round_bf16(float f)
     return (uint16_t)(u >> 16);
 }
 
-// One wave per id; each lane handles 4 consecutive int8 per iteration (dim % 4 == 0).
-__global__ __launch_bounds__(256) void embed_int8_kernel(const int8_t* __restrict__ table, const void* __restrict__ scales,
-                                                         int st, const int64_t* __restrict__ ids, void* __restrict__ out,
-                                                         long n_ids, int vocab, int dim)
+// One workgroup per id.  Each lane loads up to EMB_BATCH words (4 int8 each) of the row at
+// once and only then scales and stores them, so a row of a few thousand bytes costs one
+// memory round trip (one wave looping over a 5120-byte row waited on 20 dependent loads:
+// 13.5 us per batch-1 gather).
+constexpr int EMB_THREADS = 256;
+constexpr int EMB_BATCH = 8;
+
+__global__ __launch_bounds__(EMB_THREADS) void embed_int8_kernel(const int8_t* __restrict__ table, const void* __restrict__ scales,
+                                                                 int st, const int64_t* __restrict__ ids, void* __restrict__ out,
+                                                                 int vocab, int dim)
 {
-    const long n = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (n >= n_ids) return;
-    const int lane = threadIdx.x & 63;
+    const long n = blockIdx.x;
     const int64_t id = ids[n];
     const bool ok = id >= 0 && id < vocab;
     const float sc = ok ? load_scale(scales, id, st) : 0.f;
     const uint32_t* row = reinterpret_cast<const uint32_t*>(table + (ok ? id : 0) * (long)dim);
-    for (int q = lane; q < dim / 4; q += 64) {
-        const uint32_t v = ok ? row[q] : 0u;
-        float f[4];
+    const int nw = dim / 4;
+    for (int q0 = 0; q0 < nw; q0 += EMB_THREADS * EMB_BATCH) {
+        uint32_t v[EMB_BATCH];
 #pragma unroll
-        for (int b = 0; b < 4; b++) f[b] = (float)(int8_t)(v >> (8 * b)) * sc;
-        if (st == ST_F32) {
-            float4 o = {f[0], f[1], f[2], f[3]};
-            reinterpret_cast<float4*>(static_cast<float*>(out) + n * (long)dim)[q] = o;
-        } else {
-            uint16_t hb[4];
+        for (int b = 0; b < EMB_BATCH; b++) {
+            const int q = q0 + threadIdx.x + b * EMB_THREADS;
+            v[b] = ok && q < nw ? row[q] : 0u;
+        }
 #pragma unroll
-            for (int b = 0; b < 4; b++)
-                hb[b] = st == ST_BF16 ? round_bf16(f[b]) : __builtin_bit_cast(uint16_t, (_Float16)f[b]);
-            uint2 o = {(uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16)};
-            reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + n * (long)dim)[q] = o;
+        for (int b = 0; b < EMB_BATCH; b++) {
+            const int q = q0 + threadIdx.x + b * EMB_THREADS;
+            if (q >= nw) break;
+            float f[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) f[i] = (float)(int8_t)(v[b] >> (8 * i)) * sc;
+            if (st == ST_F32) {
+                float4 o = {f[0], f[1], f[2], f[3]};
+                reinterpret_cast<float4*>(static_cast<float*>(out) + n * (long)dim)[q] = o;
+            } else {
+                uint16_t hb[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    hb[i] = st == ST_BF16 ? round_bf16(f[i]) : __builtin_bit_cast(uint16_t, (_Float16)f[i]);
+                uint2 o = {(uint32_t)hb[0] | ((uint32_t)hb[1] << 16), (uint32_t)hb[2] | ((uint32_t)hb[3] << 16)};
+                reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + n * (long)dim)[q] = o;
+            }
         }
     }
 }
@@ -62,9 +77,9 @@ int embed_dispatch(const int8_t* table, const void* scales, int scale_dtype, con
                    void* out, long n_ids, int vocab, int dim, hipStream_t stream)
 {
     if (n_ids == 0) return EXL3_OK;
-    const long grid = (n_ids + 3) / 4;
-    hipLaunchKernelGGL(embed_int8_kernel, dim3((unsigned)grid), dim3(256), 0, stream, table, scales,
-                       scale_dtype, ids, out, n_ids, vocab, dim);
+    if (n_ids > 0x7fffffffL) return set_error(EXL3_ERR_ARG, "exl3_embed_int8_gather: %ld ids (at most 2^31 - 1)", n_ids);
+    hipLaunchKernelGGL(embed_int8_kernel, dim3((unsigned)n_ids), dim3(EMB_THREADS), 0, stream, table, scales,
+                       scale_dtype, ids, out, vocab, dim);
     return check_launch("exl3_embed_int8_gather");
 }
 

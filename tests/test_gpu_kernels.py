@@ -369,6 +369,19 @@ def test_embed_int8_gather_bit_exact(native, dtype):
     assert torch.equal(out.cpu(), want)
 
 
+def test_embed_int8_long_rows_many_ids_and_bad_ids(native):
+    # dim 8196: 2049 words, so each lane of the 256-lane workgroup takes two load batches
+    g = torch.Generator().manual_seed(10)
+    q = torch.randint(-128, 128, (300, 8196), generator=g, dtype=torch.int8)
+    s = (torch.rand(300, 1, generator=g) * 0.02).half()
+    ids = torch.randint(0, 300, (3000,), generator=g)
+    ids[[0, 1234, 2999]] = torch.tensor([-1, 300, 1 << 40])
+    out = native.embed_int8(q.to(dev()), s.to(dev()), ids.to(dev())).cpu()
+    ok = (ids >= 0) & (ids < 300)
+    assert torch.equal(out[ok], q[ids[ok]].half() * s[ids[ok]])
+    assert torch.equal(out[~ok], torch.zeros(int((~ok).sum()), 8196, dtype=torch.half))
+
+
 def test_embed_int8_config4_shape(native):
     g = torch.Generator().manual_seed(9)
     q = torch.randint(-128, 128, (syn.VOCAB, 5120), generator=g, dtype=torch.int8)
