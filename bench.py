@@ -13,7 +13,7 @@ The timed steps are replayed from a HIP graph (captured once, the way decode ser
 replays its steps), so host launch overhead is not part of the measurement; the
 warm-up steps are a graph replay too.
 `value` = total packed trellis bytes / total time over the timed steps.
-`roofline` = the dominant GEMV (the K whose calls take the most time; one call = one
+`roofline` = the dominant GEMV (the K whose call moves the most bytes; one call = one
 gemv1_kernel<K> launch and one gemv1_finish_kernel launch): algorithmic bytes per call
 (ic*oc*K/8) / its mean duration from HIP events recorded on the replay stream around a
 graph of the same steps, against 8 TB/s.  `traffic` = HBM bytes per call measured with
@@ -161,7 +161,9 @@ def gpu_bench(args) -> dict:
         del gk
     total_bytes = sum(per_k[K]["bytes"] for K in Ks) * args.steps
     value = total_bytes / wall / 1e9
-    dom = max(Ks, key=lambda K: per_k[K]["total_s"])
+    # the call that moves the most of the step's bytes (K=5 in the default run); the calls'
+    # times are within noise of each other, so the longest one changes from run to run
+    dom = max(Ks, key=lambda K: per_k[K]["bytes"])
     return dict(value=value, wall=wall, per_k=per_k, dom=dom,
                 device=torch.cuda.get_device_name(dev))
 

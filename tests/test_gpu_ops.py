@@ -265,3 +265,13 @@ def test_reconstruct_weight_matches_oracle_deploy_weight(native, oracle):
         ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
         bound = 0.5 * ulp + 2.0 ** -16 * np.abs(ref).max()
         assert (np.abs(W - ref) <= bound).all(), (K, cb, np.max(np.abs(W - ref) / bound))
+
+
+def test_min_capability_passes_vllms_check_on_this_gpu():
+    """vLLM refuses a quantization method when the device capability, major * 10 + minor,
+    is below get_min_capability() (reference orcasaq2/config.py:107-109 returns 80).  On
+    ROCm torch reports gfx9 parts as (9, x): gfx950 is (9, 5), so 95 >= 80 passes."""
+    from orcasaq2.config import Exl3Config
+    major, minor = torch.cuda.get_device_capability(0)
+    assert major * 10 + minor >= Exl3Config.get_min_capability(), (major, minor)
+    assert "gfx9" in torch.cuda.get_device_properties(0).gcnArchName
