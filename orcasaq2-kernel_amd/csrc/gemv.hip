@@ -30,7 +30,7 @@ namespace exl3 {
 
 constexpr int GV_WAVES = 4;
 constexpr int GV_MAX_ROWS = 16;
-constexpr int GV_SPLIT_MAX_ROWS = 4;                   // more rows: gemm_sk.hip, 16-row tiles
+constexpr int GV_SPLIT_MAX_ROWS = 4;                   // more rows: gemv16.hip
 constexpr int GV_MAX_BLKS = 8;                          // 128-input blocks per workgroup (even)
 constexpr int GV_HX_ROW = GV_MAX_BLKS * 8 * 16 + 4;     // u32 per LDS activation row (16 B per tile row and m)
 constexpr int GV_GROUP = 8;                             // shards per launch

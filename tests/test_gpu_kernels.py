@@ -179,7 +179,7 @@ def test_gemv_deterministic_and_workspace_rearmed(native):
 def test_gemv_grouped_config2(native, oracle, rows):
     """qkv: q K4 5120->6144, k/v K5 5120->1024; gate_up: 2 x K3 5120->17408.  Rows 2..4 take
     the 1..4-row kernel for both (gate_up at four rows with three workgroups per CU); 9 and
-    16 rows the 16-row tiles, qkv's mixed K in one launch."""
+    16 rows the 5..16-row kernel (gemv16), qkv's mixed K in one launch."""
     x = syn.activations(rows, 5120, torch.Generator().manual_seed(20 + rows))
     for spec in ([(6144, 4), (1024, 5), (1024, 5)], [(17408, 3), (17408, 3)]):
         lins = [syn.linear(5120, oc, K, seed=200 + i) for i, (oc, K) in enumerate(spec)]

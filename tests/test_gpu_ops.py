@@ -84,8 +84,8 @@ def test_hip_graph_capture_replays(native, oracle, rows):
     """The op and the grouped op captured into a HIP graph on a stream that ran them eagerly
     first (so the capture uses that stream's eager GEMV workspace), replayed four times with
     eager work between replays, against eager results: 1 row (persistent decode launch and
-    its split-segment finishing kernel), 2 rows (four-row template), 9 rows (16-row tiles,
-    one launch over both K), 40 rows (prefill: 48-row stream-K tiles, counters zeroed by the
+    its split-segment finishing kernel), 2 rows (four-row template), 9 rows (the 5..16-row
+    kernel: set-up, one decode launch over both K, finish), 40 rows (prefill: 48-row stream-K tiles, counters zeroed by the
     set-up kernels inside the graph)."""
     step = _two_shard_step(rows)
     x = syn.activations(rows, 1024, torch.Generator().manual_seed(1)).to(D)
