@@ -5,7 +5,7 @@ workgroup, so one column group can be split over several workgroups and one work
 touch several column groups (and shards).  These cases cover: a column group inside one
 workgroup, split over several, workgroups spanning 2-3 column groups and a shard
 boundary, waves left without units, every K and both codebooks, grouped shards with mixed
-K, the segment counters left at zero for the next call, determinism, and the config-4
+K, the workspace's reserved head left untouched, determinism, and the config-4
 lm_head shape (5120 -> 151936, K = 6) checked on sampled column groups.  Bar: per-row
 relative L2 error <= 1e-3 against the fp64 oracle on the same fp16 inputs.
 """
@@ -68,16 +68,42 @@ def test_gemv1_grouped_mixed_K(native, oracle):
         col += l["oc"]
 
 
-def test_gemv1_counters_left_zero_and_deterministic(native):
+@pytest.mark.parametrize("rows", [1, 3, 4])
+def test_gemv1_table_tasks_cross_several_shards(native, oracle, rows):
+    """Eight 128-output shards over 128 inputs (one input block per column group): a launch
+    of 64 units on two workgroups, whose waves' activation-table tasks step over several
+    segments at once and so cross two shard boundaries in one wave's walk (four rows: a
+    wave's tasks are occurrences 0, 2, 4 = shards 0, 2, 4)."""
+    lins = [syn.linear(128, 128, 3, seed=400 + i) for i in range(8)]
+    x = syn.activations(rows, 128, torch.Generator().manual_seed(41 + rows))
+    y = native.gemv_grouped(x.to(dev()), [dict(to_gpu(l), codebook=0) for l in lins])
+    for i, l in enumerate(lins):
+        check(y[:, 128 * i:128 * (i + 1)], x, l, 0, oracle)
+    ragged = [syn.linear(256, oc, 4, seed=420 + i) for i, oc in enumerate([384, 128, 640, 128, 256, 128, 1152, 128])]
+    x2 = syn.activations(rows, 256, torch.Generator().manual_seed(43))
+    y = native.gemv_grouped(x2.to(dev()), [dict(to_gpu(l), codebook=0) for l in ragged])
+    col = 0
+    for l in ragged:
+        check(y[:, col:col + l["oc"]], x2, l, 0, oracle)
+        col += l["oc"]
+
+
+def test_gemv1_workspace_head_untouched_and_deterministic(native):
+    """Repeated calls give identical outputs, and no kernel writes the workspace's reserved
+    16 KiB head (the workspace has no required contents: it comes from torch.empty, so the
+    head is filled with a marker here and must keep it)."""
     lin = to_gpu(syn.linear(4096, 2048, 4, seed=77))
     x = syn.activations(1, 4096, torch.Generator().manual_seed(7)).to(dev())
-    ys = [native.gemv(x, lin["trellis"], lin["suh"], lin["svh"], 4, 0) for _ in range(5)]
-    torch.cuda.synchronize()
-    for y in ys[1:]:
-        assert torch.equal(y, ys[0])
+    y0 = native.gemv(x, lin["trellis"], lin["suh"], lin["svh"], 4, 0)
     key = (0, torch.cuda.current_stream(dev()).cuda_stream)
     ws = native._gemv_ws[key]
-    assert int(ws[:16384].count_nonzero()) == 0
+    ws[:16384].fill_(0xA5)
+    ys = [native.gemv(x, lin["trellis"], lin["suh"], lin["svh"], 4, 0) for _ in range(5)]
+    torch.cuda.synchronize()
+    assert native._gemv_ws[key].data_ptr() == ws.data_ptr()
+    for y in ys:
+        assert torch.equal(y, y0)
+    assert bool((ws[:16384] == 0xA5).all())
 
 
 def test_gemv1_lm_head_sampled_column_groups(native, oracle):
