@@ -16,7 +16,8 @@
 //   1. topk_chunk_kernel, one 256-lane workgroup per 4096-column chunk of a row: the
 //      chunk's k selected go to its k candidate slots in column order (a chunk with fewer
 //      than k columns leaves its last slots 0, below every real candidate).
-//   2. topk_merge_kernel, one 512-lane workgroup per row: the same selection over the row's
+//   2. topk_merge_kernel, one workgroup per row (256 lanes for up to 4096 candidates, else
+//      512): the same selection over the row's
 //      candidates (chunk-major, so in column order), then the k selected ranked by (key,
 //      column) into the outputs.
 // A workgroup's waves share one CU and its scalar unit, which executes each wave's ballot
@@ -211,8 +212,8 @@ __global__ __launch_bounds__(TK_T1) void topk_chunk_kernel(const uint16_t* __res
     if ((int)threadIdx.x < k - nsel) out[nsel + threadIdx.x] = 0;    // a chunk of fewer than k columns
 }
 
-template <bool ARGMAX>
-__global__ __launch_bounds__(TK_T2) void topk_merge_kernel(const uint64_t* __restrict__ cand, int m, int k,
+template <bool ARGMAX, int T2>
+__global__ __launch_bounds__(T2) void topk_merge_kernel(const uint64_t* __restrict__ cand, int m, int k,
                                                             uint16_t* __restrict__ values, int64_t* __restrict__ idx)
 {
     __shared__ TkLds L;
@@ -231,7 +232,7 @@ __global__ __launch_bounds__(TK_T2) void topk_merge_kernel(const uint64_t* __res
 #pragma unroll
         for (int j = 0; j < TK_PER; j++)
             if (tk_ord(v[j]) > tk_ord(b)) b = v[j];
-        b = tk_block_argmax<TK_T2 / 64>(b, L.best);
+        b = tk_block_argmax<T2 / 64>(b, L.best);
         if (threadIdx.x == 0) {
             values[row] = (uint16_t)(b & 0xffffu);
             idx[row] = tk_cand_col(b);
@@ -239,7 +240,7 @@ __global__ __launch_bounds__(TK_T2) void topk_merge_kernel(const uint64_t* __res
         return;
     }
     int pos, nsel;
-    const uint32_t mask = tk_select<TK_T2 / 64>(key, k, L, pos, nsel);   // nsel = k: k <= n real candidates
+    const uint32_t mask = tk_select<T2 / 64>(key, k, L, pos, nsel);   // nsel = k: k <= n real candidates
 #pragma unroll
     for (int j = 0; j < TK_PER; j++)
         if (mask & (1u << j)) {
@@ -279,8 +280,13 @@ int topk_dispatch(const uint16_t* x, int rows, int n, long ld, int k, uint16_t* 
                        stream, x, ld, n, k, nchunk, cand);
     int rc = check_launch("exl3_topk (chunks)");
     if (rc != EXL3_OK) return rc;
-    hipLaunchKernelGGL(am ? topk_merge_kernel<true> : topk_merge_kernel<false>, dim3(rows), dim3(TK_T2), 0, stream,
-                       cand, nchunk * k, k, values, idx);
+    // fewer waves for fewer candidates: every wave's ballot counts run on the CU's scalar unit
+    const int m = nchunk * k;
+    const void* mk = m <= 256 * TK_PER ? (am ? (const void*)&topk_merge_kernel<true, 256> : (const void*)&topk_merge_kernel<false, 256>)
+                                       : (am ? (const void*)&topk_merge_kernel<true, TK_T2> : (const void*)&topk_merge_kernel<false, TK_T2>);
+    const uint64_t* cand_c = cand;
+    void* kargs[] = {&cand_c, const_cast<int*>(&m), &k, &values, &idx};
+    hipLaunchKernel(mk, dim3(rows), dim3(m <= 256 * TK_PER ? 256 : TK_T2), kargs, 0, stream);
     return check_launch("exl3_topk (merge)");
 }
 
