@@ -275,3 +275,27 @@ def test_min_capability_passes_vllms_check_on_this_gpu():
     major, minor = torch.cuda.get_device_capability(0)
     assert major * 10 + minor >= Exl3Config.get_min_capability(), (major, minor)
     assert "gfx9" in torch.cuda.get_device_properties(0).gcnArchName
+
+
+def test_concurrent_streams_keep_their_own_workspaces(native):
+    """Three streams (default priority) run the ops at 1, 9 and 40 rows at the same time, each
+    calling repeatedly on its own stream: every stream gets its own GEMV workspace, and every
+    result equals the one computed alone on the default stream."""
+    steps = {rows: _two_shard_step(rows) for rows in (1, 9, 40)}
+    xs = {rows: syn.activations(rows, 1024, torch.Generator().manual_seed(90 + rows)).to(D) for rows in steps}
+    want = {rows: steps[rows](xs[rows]) for rows in steps}
+    torch.cuda.synchronize()
+    streams = {rows: torch.cuda.Stream() for rows in steps}
+    for s in streams.values():
+        s.wait_stream(torch.cuda.current_stream())
+    got = {rows: [] for rows in steps}
+    for it in range(6):                                   # interleaved issue on the three streams
+        for rows, s in streams.items():
+            with torch.cuda.stream(s):
+                got[rows].append(steps[rows](xs[rows]))
+    torch.cuda.synchronize()
+    for rows in steps:
+        for a, b in got[rows]:
+            assert torch.equal(a, want[rows][0]) and torch.equal(b, want[rows][1]), rows
+    keys = [k for k in native._gemv_ws if k[1] in {s.cuda_stream for s in streams.values()}]
+    assert len({native._gemv_ws[k].data_ptr() for k in keys}) == len(keys)   # no workspace shared
