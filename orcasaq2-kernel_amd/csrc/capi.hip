@@ -19,6 +19,8 @@ int set_error(int code, const char* fmt, ...)
     return code;
 }
 
+void clear_error() { g_err[0] = 0; }
+
 int check_launch(const char* what)
 {
     const hipError_t e = hipGetLastError();

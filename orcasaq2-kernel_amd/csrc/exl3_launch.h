@@ -12,6 +12,9 @@ namespace exl3 {
 // Records a printf-style message for exl3_last_error() and returns `code`.
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 
+// Empties that message (for a refusal the caller recovers from).
+void clear_error();
+
 // Returns EXL3_OK, or records the pending launch error of `what`.
 int check_launch(const char* what);
 
@@ -35,7 +38,8 @@ struct GemvShard {
 constexpr size_t GEMV_COUNTER_BYTES = 16384;
 size_t gemv_workspace_bytes(int rows, int ic, int oc);
 size_t gemv1_slot_bytes(int ic, int oc, int rows);
-bool gemv1_rows_fit(const GemvShard* shards, int nshards, int rows);
+bool gemv1_plan_fits(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
+                     size_t slot_bytes);
 int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
                    size_t slot_bytes, hipStream_t stream);
 int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows,

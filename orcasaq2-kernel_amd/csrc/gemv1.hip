@@ -1,9 +1,8 @@
 // Fused EXL3 decode-GEMV for one to four activation rows (batch-1..4 decode):
 //   y_r (oc) = fp16( H( fp16(H(x_r * suh)) . W_q ) * svh ),  r < nrows
 // with W_q decoded from the packed trellis in registers and never stored.  Replaces
-// exllamav3_ext.exl3_gemm as called at orcasaq2/ops.py:46-49 for rows <= 4 (rows 2..4 only
-// where the launch keeps three workgroups per CU resident; gemv.hip's split kernels take
-// the rest, gemv16.hip takes 5..16 rows).
+// exllamav3_ext.exl3_gemm as called at orcasaq2/ops.py:46-49 for rows <= 4 (rows 2..4
+// wherever this plan takes the shards; gemv16.hip takes the rest and 5..16 rows).
 //
 // Work decomposition.  A *unit* is one tile row of one 128-output column group: 8 tiles
 // side by side, 64 chunks of 32 positions -- one chunk per lane of a wave, the 8 tiles'
@@ -456,28 +455,17 @@ static int g1_launch(const void* fn, void* arg, int G, size_t lds, hipStream_t s
     return check_launch("exl3_gemv (1-4 rows)");
 }
 
-// Whether 2..4 rows of these shards run well here: every launch keeps at least three
-// workgroups per CU resident (with four rows the LDS per workgroup grows with its range).
-// The caller takes the split kernels otherwise.
-bool gemv1_rows_fit(const GemvShard* shards, int nshards, int rows)
+// Whether g1_plan takes these shards at this row count: the plan run without launching
+// anything.  It refuses a launch whose workgroup ranges' activation tables would exceed a
+// CU's LDS even at G1_GMAX workgroups (with four rows, some 2.6e9 weights in one launch);
+// the refusal's message is dropped, since the caller then takes gemv16 instead.
+bool gemv1_plan_fits(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
+                     size_t slot_bytes)
 {
-    const int ntr = shards[0].ic / 16;
-    const int cus = g1_cu_count();
-    // the launches group shards of one codebook; bound each launch by all of its shards
-    for (int cb = 0; cb < 2; cb++) {
-        long U[G1_MAXSH];
-        int ns = 0, G[G1_MAXSH];
-        for (int i = 0; i < nshards; i++) {
-            if (shards[i].cb != cb) continue;
-            const long u = (long)(shards[i].oc / 128) * ntr;
-            if (ns < G1_MAXSH) U[ns++] = u;
-            else U[G1_MAXSH - 1] += u;
-        }
-        if (!ns) continue;
-        size_t lds;
-        if (g1_split(U, ns, ntr, rows, cus, G, lds) < 3) return false;
-    }
-    return true;
+    const int rc = g1_plan(A, shards, nshards, rows, slots, slot_bytes, g1_cu_count(),
+                           [](const G1Launch&) { return EXL3_OK; });
+    if (rc != EXL3_OK) clear_error();
+    return rc == EXL3_OK;
 }
 
 // The launches of g1_plan: the decode kernel, then (if some segment is split) the finish

@@ -171,6 +171,16 @@ def test_gemv16_lm_head(rl):
     ok(gemv16(rl, 16, 5120, [151936], [6]), "lm_head 16 rows")
 
 
+@pytest.mark.parametrize("rows", [2, 3, 4])
+def test_gemv_2_to_4_rows_take_gemv16_beyond_gemv1s_lds(rl, rows):
+    # exl3_gemv's routing at 2..4 rows: gemv1 wherever its plan fits, the lm_head included
+    # (more workgroups than stay resident); gemv16 for the shards gemv1's plan refuses
+    ok(gemv1(rl, rows, 5120, [151936], [6]), f"lm_head rows={rows} (gemv1)")
+    rc, msg, _ = gemv1(rl, rows, 16384, [163840], [1])
+    assert rc == 2 and "bytes of LDS per workgroup" in msg
+    ok(gemv16(rl, rows, 16384, [163840], [1]), f"16384 x 163840 rows={rows} (gemv16)")
+
+
 @pytest.mark.parametrize("K", range(1, 9))
 def test_gemv16_every_K(rl, K):
     ok(gemv16(rl, 7, 768, [384, 128], [K, K], [0, 1]), f"K={K}")

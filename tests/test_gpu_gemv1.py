@@ -6,7 +6,9 @@ touch several column groups (and shards).  These cases cover: a column group ins
 workgroup, split over several, workgroups spanning 2-3 column groups and a shard
 boundary, waves left without units, every K and both codebooks, grouped shards with mixed
 K, the workspace's reserved head left untouched, determinism, and the config-4
-lm_head shape (5120 -> 151936, K = 6) checked on sampled column groups.  Bar: per-row
+lm_head shape (5120 -> 151936, K = 6) checked on sampled column groups, at 1 row and at
+2..4 rows (the four-row template on more workgroups than stay resident); and a shard too
+large for the four-row template's LDS, which 2..4-row calls hand to gemv16.  Bar: per-row
 relative L2 error <= 1e-3 against the fp64 oracle on the same fp16 inputs.
 """
 import numpy as np
@@ -122,12 +124,12 @@ def test_gemv1_lm_head_sampled_column_groups(native, oracle):
         check(y[:, sl], x, lin, 0, oracle)
 
 
-@pytest.mark.parametrize("rows", [2, 4])
-def test_gemv_split_kernels_on_a_wide_shard(native, oracle, rows):
-    """2..4 rows of the lm_head shape (5120 -> 151936, K=6): with four activation rows its
-    workgroup ranges would need more LDS than three resident workgroups per CU leave, so the
-    call takes the split kernels (gemv_partial_kernel + gemv_reduce_kernel); four column
-    groups are checked against the oracle on the matching trellis slice."""
+@pytest.mark.parametrize("rows", [2, 3, 4])
+def test_gemv1_2_to_4_rows_on_the_lm_head(native, oracle, rows):
+    """2..4 rows of the lm_head shape (5120 -> 151936, K=6): with four activation rows a
+    workgroup range's tables leave fewer than three workgroups per CU resident, so the launch
+    takes G1_GMAX workgroups that run in turn; four column groups are checked against the
+    oracle on the matching trellis slice."""
     ic, oc, K = 5120, 151936, 6
     g = torch.Generator().manual_seed(5)
     t = syn.trellis(ic, oc, K, g)
@@ -139,3 +141,31 @@ def test_gemv_split_kernels_on_a_wide_shard(native, oracle, rows):
         sl = slice(cg * 128, (cg + 1) * 128)
         lin = dict(trellis=t[:, cg * 8:(cg + 1) * 8].contiguous(), suh=suh, svh=svh[sl].contiguous(), K=K)
         check(y[:, sl], x, lin, 0, oracle)
+
+
+def test_gemv_2_to_4_rows_beyond_gemv1s_lds_take_gemv16(native, oracle):
+    """A 16384 -> 163840 shard (K=1, 2.7e9 weights): at 2..4 rows gemv1's plan refuses it
+    (a workgroup range's activation tables would exceed a CU's LDS even at G1_GMAX
+    workgroups) and the call takes gemv16.  Sampled column groups against the oracle, and
+    every column against the same rows run one at a time through gemv1."""
+    ic, oc, K = 16384, 163840, 1
+    g = torch.Generator(device=dev()).manual_seed(9)
+    t = torch.randint(-32768, 32768, (ic // 16, oc // 16, 16 * K), generator=g, device=dev(),
+                      dtype=torch.int32).to(torch.int16)
+    gc = torch.Generator().manual_seed(10)
+    suh = syn.signs(ic, gc)
+    svh = syn.svh(ic, oc, gc)
+    sd, vd = suh.to(dev()), svh.to(dev())
+    for rows in (2, 3, 4):
+        print(f"gemv rows={rows} 16384 x 163840 K=1", flush=True)
+        x = syn.activations(rows, ic, torch.Generator().manual_seed(60 + rows))
+        xd = x.to(dev())
+        y = native.gemv(xd, t, sd, vd, K, 0)
+        y1 = torch.cat([native.gemv(xd[r:r + 1], t, sd, vd, K, 0) for r in range(rows)])
+        num = (y.float() - y1.float()).norm(dim=1)
+        assert bool((num <= 1e-3 * y1.float().norm(dim=1)).all()), num
+        y = y.cpu()
+        for cg in (0, 311, 1279):
+            sl = slice(cg * 128, (cg + 1) * 128)
+            lin = dict(trellis=t[:, cg * 8:(cg + 1) * 8].cpu().contiguous(), suh=suh, svh=svh[sl].contiguous(), K=K)
+            check(y[:, sl], x, lin, 0, oracle)
