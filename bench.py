@@ -30,6 +30,7 @@ one HIP graph, replayed (attention excluded).
     python bench.py --workload config2   # grouped qkv / gate_up GEMVs at batch 1, 4, 16
     python bench.py --workload config3   # M=2048 prefill GEMM (TFLOP/s, MFMA share) + reconstruct
     python bench.py --workload config4   # the 64-layer batch-1 linear stack alone (tok/s-equivalent)
+    python bench.py --workload lmhead    # the K=6 lm_head GEMV at 1, 2, 3, 4, 8, 16 rows
     python bench.py --workload prefill   # 17..768-row prefill: fused vs reconstruct branch, grouped layers
     python bench.py --workload ceiling   # what bounds batch 1: loads / decode / MFMA alone, instruction costs
 print their own JSON line instead of the headline line.
@@ -380,6 +381,40 @@ def config2_bench(reps: int) -> dict:
     return out
 
 
+def lmhead_bench(reps: int) -> dict:
+    """The K=6 lm_head (5120 -> 151936, 583 MB packed) as one GEMV at 1, 2, 3, 4, 8 and 16
+    rows: 1..4 rows on the four-row decode kernel (with 2..4 rows its workgroup ranges' tables
+    leave fewer than three workgroups per CU resident, so the launch takes more workgroups
+    than stay resident), 5..16 on gemv16.  Each call reads a different weight copy."""
+    import torch
+    from orcasaq2 import _native
+    from orcasaq2 import synthetic as syn
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(6)
+    H, V, K = syn.HIDDEN, syn.VOCAB, 6
+    nbytes = syn.packed_bytes(H, V, K)
+    n = max(2, math.ceil(ROTATE_BYTES / nbytes))
+    copies = [_rand_linear(H, V, K, g, dev) for _ in range(n)]
+    out = {}
+    for rows in (1, 2, 3, 4, 8, 16):
+        x = torch.randn(rows, H, generator=g, device=dev).half()
+        y = torch.empty(rows, V, dtype=torch.half, device=dev)
+
+        def run():
+            for c in copies:
+                _native.gemv(x, c["trellis"], c["suh"], c["svh"], K, 0, out=y)
+
+        graph, side = _graph(dev, run)
+        sec = _time_graph(graph, side, max(1, reps // n)) / n
+        del graph
+        out[f"b{rows}"] = {"us_per_call": round(sec * 1e6, 3), "packed_bytes": nbytes,
+                           "GB/s": round(nbytes / sec / 1e9, 1),
+                           "frac": round(nbytes / sec / 1e9 / HBM_PEAK_GBS, 4)}
+    del copies
+    return out
+
+
 def config3_bench(reps: int) -> dict:
     """Config 3: prefill GEMM of M=2048 rows through down_proj (17408 -> 5120, K=4), and a
     standalone reconstruct of the same weight to fp16, as (ic, oc) and as (oc, ic)."""
@@ -640,7 +675,7 @@ def main():
     ap.add_argument("--only-K", type=int, default=0, help="time a single K (profiling runs)")
     ap.add_argument("--copy-calib", action="store_true", help="run the counter-calibration copy and exit")
     ap.add_argument("--workload", default="config1",
-                    choices=("config1", "config2", "config3", "config4", "prefill", "ceiling"),
+                    choices=("config1", "config2", "config3", "config4", "lmhead", "prefill", "ceiling"),
                     help="config1 = the headline line (+ the config-4 stack); config2/config3/config4 "
                          "print their own measurement line")
     ap.add_argument("--no-stack", action="store_true", help="skip the config-4 stack measurement")
@@ -653,9 +688,10 @@ def main():
     if args.copy_calib:
         copy_calib(args)
         return
-    if args.workload in ("config2", "config3", "config4", "prefill", "ceiling"):
+    if args.workload in ("config2", "config3", "config4", "lmhead", "prefill", "ceiling"):
         import torch
         res = (config2_bench(args.steps * 5) if args.workload == "config2" else
+               lmhead_bench(args.steps * 5) if args.workload == "lmhead" else
                ceiling_bench(args.steps) if args.workload == "ceiling" else
                config3_bench(args.steps) if args.workload == "config3" else
                prefill_bench(args.steps) if args.workload == "prefill" else stack_bench(args.steps))
