@@ -14,7 +14,8 @@
 // its 16-byte fragments of a unit from there (L2-resident: 64 KB per 1024 inputs per shard).
 //
 // Work decomposition as in gemv1.hip: units numbered shard, strip (32 outputs), then unit
-// down the strip; G nearly equal contiguous ranges, one per workgroup of 8 waves, each wave a
+// down the strip; G nearly equal contiguous ranges, one per workgroup of 8 waves (at odd K a
+// launch of one group hands the workgroups to its blocks XCD by XCD, g16_block_wg), each wave a
 // contiguous run, one unit in flight per wave.  A wave's partials of a strip go to
 // red[strip + wave] in LDS; per strip the workgroup adds them in wave order into its slot.
 // gemv16_finish_kernel then adds each strip's slots in workgroup order (deterministic) and,
@@ -160,7 +161,7 @@ template <int K, int CB, bool ONE>
 __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8), amdgpu_num_sgpr(74))) void gemv16_kernel(const G16Args a)
 {
     extern __shared__ __attribute__((aligned(16))) float g16_red[];
-    g16_body<K, CB, ONE>(a.grp, a.sh, blockIdx.x, g16_red);
+    g16_body<K, CB, ONE>(a.grp, a.sh, g16_block_wg(blockIdx.x, gridDim.x, K), g16_red);
 }
 
 template <int CB>

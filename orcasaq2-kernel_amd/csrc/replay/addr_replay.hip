@@ -1138,7 +1138,11 @@ int exl3r_gemv16(int rows, int ic, int nshards, const int* oc, const int* K, con
             if (L.lds > G1_LDS_PER_CU) fail("gemv16 launch %d: %zu bytes of LDS", launch, L.lds);
             if (!L.multi) {
                 const G1Group& a = L.args->grp;
-                for (int g = 0; g < L.G; g++) {
+                std::vector<char> wg_seen(L.G, 0);
+                for (int blk = 0; blk < L.G; blk++) {   // the kernel's block -> workgroup order
+                    const int g = g16_block_wg(blk, L.G, L.K);
+                    if (g < 0 || g >= L.G || wg_seen[g]++)
+                        fail("gemv16 launch %d: block %d -> workgroup %d of %d", launch, blk, g, L.G);
                     if (L.one) g16_replay_wg_k<true>(L.K, W, shards.data(), a, L.args->sh, g, L.lds, launch);
                     else g16_replay_wg_k<false>(L.K, W, shards.data(), a, L.args->sh, g, L.lds, launch);
                 }
