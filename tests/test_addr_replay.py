@@ -181,6 +181,14 @@ def test_gemv_2_to_4_rows_take_gemv16_beyond_gemv1s_lds(rl, rows):
     ok(gemv16(rl, rows, 16384, [163840], [1]), f"16384 x 163840 rows={rows} (gemv16)")
 
 
+@pytest.mark.parametrize("cus", [256, 8, 1])
+def test_gemv16_odd_K_block_order(rl, cus):
+    # one odd-K group of 1472 units: 46 workgroups, which the blocks take XCD by XCD (the
+    # replay walks the blocks in that order and checks it is a bijection)
+    ok(gemv16(rl, 7, 1024, [2944], [3], cus=cus), f"1024 x 2944 K=3 on {cus} CUs")
+    ok(gemv16(rl, 13, 1024, [1408, 1536], [7, 7], cus=cus), f"two K=7 shards on {cus} CUs")
+
+
 @pytest.mark.parametrize("K", range(1, 9))
 def test_gemv16_every_K(rl, K):
     ok(gemv16(rl, 7, 768, [384, 128], [K, K], [0, 1]), f"K={K}")

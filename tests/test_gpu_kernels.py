@@ -208,12 +208,15 @@ def test_gemv1_workgroup_ranges(native, oracle, ic, ocs, K, rows):
 
 
 @pytest.mark.parametrize("ic,ocs,K", [(128, [131200], 2), (256, [384, 128, 640], 3), (384, [1152], 5),
-                                      (2048, [128], 4), (256, [2048, 2048], 4), (640, [128, 256, 128], 6)])
+                                      (2048, [128], 4), (256, [2048, 2048], 4), (640, [128, 256, 128], 6),
+                                      (1024, [2944], 3), (1024, [1408, 1536], 7)])
 @pytest.mark.parametrize("rows", [7, 13])
 def test_gemv16_workgroup_ranges(native, oracle, ic, ocs, K, rows):
     """5..16 rows (gemv16.hip) on the range-boundary shapes of the 1..4-row test: ranges that
     span several strips and shards, start inside a strip, or cover a whole launch; strips with
-    one and with many contributing workgroups."""
+    one and with many contributing workgroups.  The last two are one odd-K group of 1472
+    units on 46 workgroups, which the blocks take XCD by XCD (5 per XCD and 6 more: both
+    parts of the block order)."""
     x = syn.activations(rows, ic, torch.Generator().manual_seed(ic + K + rows))
     lins = [syn.linear(ic, oc, K, seed=350 + i) for i, oc in enumerate(ocs)]
     shards = [dict(to_gpu(l), codebook=0) for l in lins]
