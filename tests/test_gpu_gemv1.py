@@ -1,4 +1,5 @@
-"""GPU parity of the batch-1 decode-GEMV (one activation row), through the C ABI.
+"""GPU parity of the 1..4-row decode-GEMV (gemv1.hip), mostly at one activation row, through
+the C ABI.
 
 The batch-1 kernel cuts a launch's tile-row units into equal contiguous ranges, one per
 workgroup, so one column group can be split over several workgroups and one workgroup can
