@@ -117,6 +117,20 @@ def test_workspace_sizes(native):
     assert L.exl3_gemm_workspace_bytes(2048, 17408, 5120) >= 2048 * 17408 * 2
 
 
+@pytest.mark.parametrize("ic,oc", [(5120, 6144), (5120, 1024), (17408, 5120), (5120, 151936), (16384, 163840),
+                                   (128, 128)])
+def test_gemv_workspace_at_2_to_4_rows_covers_the_gemv16_fallback(native, ic, oc):
+    """A 2..4-row call runs gemv1 where its plan takes the shards and gemv16 where it does not
+    (the choice is made per call, after the caller sized the workspace), so the 2..4-row size
+    holds gemv16's: the 5..16-row size, which does not depend on the row count."""
+    L = native.lib()
+    b16 = L.exl3_gemv_workspace_bytes(16, ic, oc)
+    assert L.exl3_gemv_workspace_bytes(5, ic, oc) == b16
+    for rows in (2, 3, 4):
+        b = L.exl3_gemv_workspace_bytes(rows, ic, oc)
+        assert b >= b16 and b >= L.exl3_gemv_workspace_bytes(1, ic, oc) and b % 256 == 0
+
+
 def test_wrappers_refuse_cpu_tensors(native):
     import torch
     x = torch.zeros(1, 128, dtype=torch.float16)
