@@ -3,6 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "exl3_common.h"
 #include "exl3_launch.h"
 
@@ -26,6 +28,30 @@ int check_launch(const char* what)
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return set_error(EXL3_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
     return EXL3_OK;
+}
+
+// Compute units of the current device, queried once per device (every plan asks on every
+// call).
+int device_cus()
+{
+    constexpr int MAXDEV = 64;
+    static int cus_of[MAXDEV];
+    static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAXDEV) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (cus_of[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+            (void)hipGetLastError();
+            cus = 256;
+        }
+        cus_of[dev] = cus;
+    }
+    return cus_of[dev];
 }
 
 static bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }

@@ -18,6 +18,9 @@ void clear_error();
 // Returns EXL3_OK, or records the pending launch error of `what`.
 int check_launch(const char* what);
 
+// Compute units of the current device (queried once per device).
+int device_cus();
+
 int reconstruct_dispatch(uint16_t* W, const uint32_t* trellis, int ic, int oc, int K, int cb, bool transposed,
                          hipStream_t stream);
 int had_dispatch(const uint16_t* in, uint16_t* out, const uint16_t* pre, const uint16_t* post,

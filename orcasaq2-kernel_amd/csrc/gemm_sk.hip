@@ -389,13 +389,7 @@ void gemm_sk_kernel(const SkArgs a)
 
 // ---------------------------------------------------------------- host side
 
-int gemm_sk_cus()
-{
-    int dev = 0, cus = 0;
-    hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    return cus;
-}
+int gemm_sk_cus() { return device_cus(); }
 
 size_t gemm_sk_slot_bytes(int rows, int oc) { return sk_single_bytes(rows, oc, gemm_sk_cus()); }
 

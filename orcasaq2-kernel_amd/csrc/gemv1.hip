@@ -423,21 +423,6 @@ static const void* g1_fn_kcb(int K, int cb, bool one)
     return nullptr;
 }
 
-static int g1_cu_count()
-{
-    struct Entry { int dev, cus; };
-    static thread_local Entry seen[16];
-    static thread_local int nseen = 0;
-    int dev = 0;
-    hipGetDevice(&dev);
-    for (int i = 0; i < nseen; i++)
-        if (seen[i].dev == dev) return seen[i].cus;
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    if (nseen < 16) seen[nseen++] = Entry{dev, cus};
-    return cus;
-}
-
 size_t gemv1_slot_bytes(int ic, int oc, int rows)
 {
     (void)ic;
@@ -462,7 +447,7 @@ static int g1_launch(const void* fn, void* arg, int G, size_t lds, hipStream_t s
 bool gemv1_plan_fits(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
                      size_t slot_bytes)
 {
-    const int rc = g1_plan(A, shards, nshards, rows, slots, slot_bytes, g1_cu_count(),
+    const int rc = g1_plan(A, shards, nshards, rows, slots, slot_bytes, device_cus(),
                            [](const G1Launch&) { return EXL3_OK; });
     if (rc != EXL3_OK) clear_error();
     return rc == EXL3_OK;
@@ -473,7 +458,7 @@ bool gemv1_plan_fits(const uint16_t* A, const GemvShard* shards, int nshards, in
 int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
                    size_t slot_bytes, hipStream_t stream)
 {
-    return g1_plan(A, shards, nshards, rows, slots, slot_bytes, g1_cu_count(), [&](const G1Launch& L) {
+    return g1_plan(A, shards, nshards, rows, slots, slot_bytes, device_cus(), [&](const G1Launch& L) {
         const char* what = "exl3_gemv (1-4 rows, split segments)";
         if (!L.multi) {
             G1Args args = *L.args;

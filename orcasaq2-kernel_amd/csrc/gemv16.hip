@@ -290,13 +290,6 @@ static const void* g16_fn_kcb(int K, int cb, bool one)
     return nullptr;
 }
 
-static int g16_cus()
-{
-    int dev = 0, cus = 0;
-    hipGetDevice(&dev);
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
-    return cus;
-}
 
 size_t gemv16_shard_bytes(int ic, int oc) { return g16_shard_bytes(ic, oc); }
 
@@ -306,7 +299,7 @@ int gemv16_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int
     const char* what = "exl3_gemv (5-16 rows)";
     G16Prep prep;
     bool prepped = false;
-    return g16_plan(A, shards, nshards, rows, ws, ws_bytes, g16_cus(), prep, [&](const G16Launch& L) {
+    return g16_plan(A, shards, nshards, rows, ws, ws_bytes, device_cus(), prep, [&](const G16Launch& L) {
         if (!prepped) {
             const long waves = (long)prep.nsh * prep.rows * prep.nblk;
             hipLaunchKernelGGL(gemv16_prep_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, prep);

@@ -170,12 +170,20 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 # GEMV workspaces.  A workspace has no required contents; one buffer serves every call
 # issued in order on one stream.
 #   _gemv_ws[(device, stream)]            made by an eager call.
-#   _gemv_ws_cap[(device, stream, id)]    made inside graph capture `id` because the
-#                                         stream had no large-enough eager workspace (its
-#                                         memory comes from that graph's pool), so it is
-#                                         used by that capture only.
-# A workspace that a captured graph uses is never freed (_gemv_ws_kept): the graph's
-# replays keep writing to it after the eager side has moved on to a larger buffer.
+#   _gemv_ws_cap[(device, stream)]        (capture id, workspace) made inside a graph capture
+#                                         because the stream had no large-enough eager
+#                                         workspace.  Its memory comes from that graph's pool,
+#                                         which keeps it for as long as the graph lives, so the
+#                                         entry serves that capture only and is simply replaced
+#                                         by the next capture on the stream (the memory may
+#                                         then go to tensors of later captures into the same
+#                                         pool, which torch replays one graph at a time; a
+#                                         workspace's contents matter within one call only).
+# An eager workspace that a captured graph uses is never freed (_gemv_ws_kept): the graph's
+# replays keep writing to it after the eager side has moved on to a larger buffer, and an
+# eager free would hand it to unrelated tensors.  That list grows only when a captured
+# stream's eager workspace is outgrown, so it holds at most one buffer per size step a
+# process takes, however many graphs it captures and destroys.
 _gemv_ws: dict = {}
 _gemv_ws_cap: dict = {}
 _gemv_ws_captured: set = set()
@@ -189,6 +197,10 @@ def capture_id(device: torch.device) -> int:
     return int(cid.value)
 
 
+def _new_gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    return torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+
+
 def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """The GEMV workspace for a call on the current stream of `device` (see above).  Calls on
     one stream run in order, so they can share one; another stream gets its own, and so does
@@ -200,21 +212,17 @@ def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     cid = capture_id(device) if torch.cuda.is_current_stream_capturing() else 0
     if cid:
         if ws is None or ws.numel() < nbytes:
-            ckey = (dev, stream, cid)
-            ws = _gemv_ws_cap.get(ckey)
-            if ws is None or ws.numel() < nbytes:
-                if ws is not None:
-                    _gemv_ws_kept.append(ws)
-                ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-                _gemv_ws_cap[ckey] = ws
-                _gemv_ws_kept.append(ws)
-            return ws
+            ent = _gemv_ws_cap.get(key)
+            if ent is None or ent[0] != cid or ent[1].numel() < nbytes:
+                ent = (cid, _new_gemv_workspace(device, nbytes))
+                _gemv_ws_cap[key] = ent
+            return ent[1]
         if ws.data_ptr() not in _gemv_ws_captured:
             _gemv_ws_captured.add(ws.data_ptr())
             _gemv_ws_kept.append(ws)
         return ws
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        ws = _new_gemv_workspace(device, nbytes)
         _gemv_ws[key] = ws
     return ws
 

@@ -169,6 +169,35 @@ def test_capture_without_eager_warmup(native):
         assert torch.equal(e2[0], eager[0]) and torch.equal(e2[1], eager[1]), i
 
 
+def test_many_captures_keep_bounded_workspace_bookkeeping(native):
+    """Graph after graph captured on fresh streams (no eager workspace there, so each capture
+    makes its own from its graph's pool): the library keeps one capture entry per stream and
+    keeps no capture workspace alive itself (the graphs' pools do), and every graph still
+    replays to the eager result after all the later captures and their destruction."""
+    step = _two_shard_step(1)
+    x = syn.activations(1, 1024, torch.Generator().manual_seed(22)).to(D)
+    eager = step(x)
+    kept0 = len(native._gemv_ws_kept)
+    graphs = []
+    for i in range(12):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            out = step(x)
+        graphs.append((g, s, out))
+        if i % 3 == 2:
+            graphs.pop(0)            # a graph destroyed along the way
+    torch.cuda.synchronize()
+    assert len(native._gemv_ws_kept) == kept0
+    assert all(isinstance(e, tuple) and len(e) == 2 for e in native._gemv_ws_cap.values())
+    for g, s, out in graphs:
+        with torch.cuda.stream(s):
+            g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out[0], eager[0]) and torch.equal(out[1], eager[1])
+
+
 def test_torch_compile_treats_op_as_opaque(native):
     lin = on(syn.linear(256, 256, 3, seed=4))
     x = syn.activations(1, 256, torch.Generator().manual_seed(4)).to(D)
