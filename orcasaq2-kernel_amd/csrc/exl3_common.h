@@ -490,6 +490,38 @@ __device__ __forceinline__ void wave_fwht128(float& v0, float& v1)
     wave_fwht128(v0, v1, fwht_signs(lane));
 }
 
+// N independent transforms round by round: each round's 2N lane exchanges are in flight
+// together, where N calls of wave_fwht128 one after another wait out N chains of six
+// exchange round trips.
+template <int N>
+__device__ __forceinline__ void wave_fwht128_n(float (&v0)[N], float (&v1)[N], const FwhtSigns& f)
+{
+#pragma unroll
+    for (int r = 0; r < N; r++) {
+        const float a = v0[r] + v1[r], b = v0[r] - v1[r];
+        v0[r] = a;
+        v1[r] = b;
+    }
+#pragma unroll
+    for (int r = 0; r < N; r++) fwht_round<1>(v0[r], v1[r], f.s[0]);
+#pragma unroll
+    for (int r = 0; r < N; r++) fwht_round<2>(v0[r], v1[r], f.s[1]);
+#pragma unroll
+    for (int r = 0; r < N; r++) fwht_round<4>(v0[r], v1[r], f.s[2]);
+#pragma unroll
+    for (int r = 0; r < N; r++) fwht_round<8>(v0[r], v1[r], f.s[3]);
+#pragma unroll
+    for (int r = 0; r < N; r++) fwht_round<16>(v0[r], v1[r], f.s[4]);
+#pragma unroll
+    for (int r = 0; r < N; r++) fwht_round<32>(v0[r], v1[r], f.s[5]);
+    const float norm = 0.08838834764831845f;  // 1/sqrt(128)
+#pragma unroll
+    for (int r = 0; r < N; r++) {
+        v0[r] *= norm;
+        v1[r] *= norm;
+    }
+}
+
 __device__ __forceinline__ f32x4 mfma16x16x32(const f16x8& a, const f16x8& b, const f32x4& c)
 {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);

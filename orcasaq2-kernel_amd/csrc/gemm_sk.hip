@@ -28,6 +28,8 @@
 #include "exl3_common.h"
 #include "gemm_sk_plan.h"
 
+#include <stdlib.h>
+
 namespace exl3 {
 
 __global__ void sk_clear_kernel(uint32_t* counters, int n)
@@ -123,6 +125,183 @@ __device__ __forceinline__ void sk_load(uint32_t (&w)[K + 1], const uint32_t* __
     } else if constexpr (K % 4 == 1) {
         w[i + 1] = p[i];
     }
+}
+
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits for this
+// wave's global stores to complete (a workgroup-scope release), which in the epilogue's
+// store loop put a store round trip into every row block.
+__device__ __forceinline__ void sk_lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// The end of a tile piece: a whole tile is finished by its workgroup; a partial piece leaves
+// its accumulators in the workgroup's slot, and the last of the tile's workgroups to arrive
+// (an agent-scope counter per tile) adds the slots in workgroup order -- deterministic --
+// and finishes the tile.  Epilogue per 128-output block: rows through LDS, FWHT across a
+// wave, * svh, fp16 store.  RBCOL: the accumulators hold the register-B kernel's output
+// columns (sk_rb_wcol) instead of 16 consecutive outputs per block.
+template <int BM, bool RBCOL>
+__device__ __forceinline__ void sk_finish_piece(const SkArgs& a, const SkPiece& pc, const SkShard& S, int g, int wave,
+                                                int lane, int tid, int wm, int wn,
+                                                f32x4 (&acc)[SkCfg<BM>::MB][SkCfg<BM>::NB], uint32_t* lds)
+{
+    constexpr int MB = SkCfg<BM>::MB, NB = SkCfg<BM>::NB;
+    const int t = pc.t, s0 = pc.s0, s1 = pc.s1, tn = pc.tn, m0 = pc.m0, tc = pc.tc;
+    // ---- finish: a whole tile here, a piece through the slots
+    bool finish = s0 == 0 && s1 == a.nks;
+    if (!finish) {
+        const int g_lo = sk_wg_of(a, (long)t * a.nks), g_hi = sk_wg_of(a, (long)(t + 1) * a.nks - 1);
+        uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + sk_slot<BM>(t, g, wave)) + lane;
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                const f32x4 v = acc[mb][nb];
+                __hip_atomic_store(my + (long)((mb * NB + nb) * 2) * 64, sk_pack2(v.x, v.y), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(my + (long)((mb * NB + nb) * 2 + 1) * 64, sk_pack2(v.z, v.w), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            }
+        __builtin_amdgcn_s_waitcnt(0);   // this wave's slot stores are complete
+        __syncthreads();                  // ... and every wave's
+        if (tid == 0) {
+            const uint32_t old = __hip_atomic_fetch_add(a.counters + t, 1u, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+            lds[0] = old == (uint32_t)(g_hi - g_lo) ? 1u : 0u;
+        }
+        __syncthreads();
+        finish = lds[0] != 0u;
+        __syncthreads();                  // lds[0] read by all before LDS is reused
+        if (finish) {
+            // last to arrive: every contributor's stores completed before its increment
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            // Slots in workgroup order, each read in batches of SK_RB 8-byte loads per lane
+            // that are all issued before the first add (atomic loads keep program order,
+            // so loads interleaved with the adds would have two in flight at a time).
+            constexpr int NP = MB * NB * 2;                   // 8-byte words per lane and slot
+            constexpr int RB = NP < 16 ? NP : 16;
+            for (int gg = g_lo; gg <= g_hi; gg++) {
+                const uint64_t* sl =
+                    reinterpret_cast<const uint64_t*>(a.slots + sk_slot<BM>(t, gg, wave)) + lane;
+#pragma unroll
+                for (int b0 = 0; b0 < NP; b0 += RB) {
+                    uint64_t v[RB];
+#pragma unroll
+                    for (int i = 0; i < RB; i++)
+                        v[i] = __hip_atomic_load(sl + (long)(b0 + i) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+                    for (int i = 0; i < RB; i += 2) {
+                        const int blk = (b0 + i) >> 1, mb = blk / NB, nb = blk % NB;
+                        acc[mb][nb] += f32x4{__builtin_bit_cast(float, (uint32_t)v[i]),
+                                             __builtin_bit_cast(float, (uint32_t)(v[i] >> 32)),
+                                             __builtin_bit_cast(float, (uint32_t)v[i + 1]),
+                                             __builtin_bit_cast(float, (uint32_t)(v[i + 1] >> 32))};
+                    }
+                }
+            }
+        }
+    }
+    if (finish) {
+        // in registers: the LDS barriers below clobber memory, which would reload these
+        uint16_t* const Cp = S.C;
+        const long ldc = S.ldc;
+        const int rows = a.rows;
+        // svh pair of this lane in the 128-output block starting at tile column ob, read
+        // once per block: the fp16 output stores could alias it, so a load inside the
+        // row loop would be repeated (a round trip per row)
+        auto load_sv = [&](int ob) -> uint32_t {
+            return ob < tc ? reinterpret_cast<const uint32_t*>(S.svh + ob * 16)[lane] : 0u;
+        };
+        int lane_v = lane;
+        asm volatile("" : "+v"(lane_v));   // the signs stay out of the main loop
+        const FwhtSigns fs = fwht_signs(lane_v);
+        // The block's svh pair as floats, converted once: a conversion left inside the store
+        // loop waits there for the load, and so for every store issued before it.
+        struct Sv {
+            float s0, s1;
+        };
+        auto load_svf = [&](int ob) -> Sv {
+            const uint32_t sv = load_sv(ob);
+            Sv r{(float)__builtin_bit_cast(_Float16, (uint16_t)(sv & 0xffffu)),
+                 (float)__builtin_bit_cast(_Float16, (uint16_t)(sv >> 16))};
+            asm volatile("" : "+v"(r.s0), "+v"(r.s1));
+            return r;
+        };
+        auto store_row = [&](int row, int ob, const Sv& sv, float v0, float v1) {
+            // ob: tile column of the 128-output block's first output; v0, v1 transformed
+            if (ob < tc && row < rows) {
+                const float sv0 = sv.s0, sv1 = sv.s1;
+                const uint32_t o = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v0 * sv0)) |
+                                   ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v1 * sv1)) << 16);
+                reinterpret_cast<uint32_t*>(Cp + (long)row * ldc + ob * 16)[lane] = o;
+            }
+        };
+        __syncthreads();                  // every wave is done with the A/B tiles
+        if constexpr (BM == 256) {
+            // Output block of rows 128 wm ..: waves wn = 2 blk and 2 blk + 1 hold its two
+            // 64-column halves.  16 rows at a time through LDS (16 x 132 floats per block
+            // and row half), then wave (wn & 1) transforms rows 8 (wn & 1) .. + 7.
+            const int blk = wn >> 1, half = wn & 1;
+            const Sv sv = load_svf(16 * tn + 8 * blk);
+            float* cs = reinterpret_cast<float*>(lds) + sk_c256(wm, blk, 0, 0);
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++) {
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        cs[sk_c256(0, 0, 4 * (lane >> 4) + e, 64 * half + (RBCOL ? sk_rb_wcol(nb, lane) : 16 * nb + (lane & 15)))] =
+                                acc[mb][nb][e];
+                sk_lds_barrier();
+                float v0[8], v1[8];                // eight independent transforms
+#pragma unroll
+                for (int r = 0; r < 8; r++) {
+                    v0[r] = cs[sk_c256(0, 0, 8 * half + r, 2 * lane)];
+                    v1[r] = cs[sk_c256(0, 0, 8 * half + r, 2 * lane + 1)];
+                }
+                wave_fwht128_n<8>(v0, v1, fs);
+#pragma unroll
+                for (int r = 0; r < 8; r++)
+                    store_row(m0 + 128 * wm + 16 * mb + 8 * half + r, 16 * tn + 8 * blk, sv, v0[r], v1[r]);
+                sk_lds_barrier();
+            }
+        } else {
+            // 16 rows at a time through LDS (16 rows of 260 floats); wave w transforms the
+            // chunk's (row, block) pairs w, w + 8, w + 16, w + 24
+            float* cs = reinterpret_cast<float*>(lds);
+            const Sv sv[2] = {load_svf(16 * tn), load_svf(16 * tn + 8)};
+#pragma unroll
+            for (int mb = 0; mb < MB; mb++) {
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        cs[sk_cx(4 * (lane >> 4) + e, NB * 16 * wn + 16 * nb + (lane & 15))] = acc[mb][nb][e];
+                sk_lds_barrier();
+                float v0[4], v1[4];                // four independent transforms
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const int j = wave + SK_WAVES * jj;
+                    const int r = j & 15, blk = j >> 4;
+                    v0[jj] = cs[sk_cx(r, 128 * blk + 2 * lane)];
+                    v1[jj] = cs[sk_cx(r, 128 * blk + 2 * lane + 1)];
+                }
+                wave_fwht128_n<4>(v0, v1, fs);
+#pragma unroll
+                for (int jj = 0; jj < 4; jj++) {
+                    const int j = wave + SK_WAVES * jj;
+                    const int r = j & 15, blk = j >> 4;
+                    store_row(m0 + 16 * mb + r, 16 * tn + 8 * blk, sv[blk], v0[jj], v1[jj]);
+                }
+                if (mb + 1 < MB) sk_lds_barrier();
+            }
+        }
+    }
+    sk_lds_barrier();                     // LDS is free for the next piece
 }
 
 // K > 0: every shard of the launch has K bits per weight; K = 0: each tile piece takes its
@@ -262,128 +441,258 @@ void gemm_sk_kernel(const SkArgs a)
         }
         u += s1 - s0;
 
-        // ---- finish: a whole tile here, a piece through the slots
-        bool finish = s0 == 0 && s1 == a.nks;
-        if (!finish) {
-            const int g_lo = sk_wg_of(a, (long)t * a.nks), g_hi = sk_wg_of(a, (long)(t + 1) * a.nks - 1);
-            uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + sk_slot<BM>(t, g, wave)) + lane;
+        sk_finish_piece<BM, false>(a, pc, S, g, wave, lane, tid, wm, wn, acc, lds);
+    }
+}
+
+// ---------------------------------------------------------------- 256-row tiles, B in registers
+//
+// The same stream-K ranges, pieces, slots and epilogue as gemm_sk_kernel<K, CB, 256>; only the
+// K-step differs.  The B tile is never stored whole to LDS: each lane decodes one chunk per
+// K-step (sk_rb_*), and the chunk's four 8-row fragments are MFMA B operands straight from
+// its registers -- the MFMA's four k-groups take four tile rows, so a lane's chunk lines up
+// with its own operand slots.  The two waves that share a wave's outputs (rows 0-127 and
+// 128-255 of the same 64 outputs) split the decode: each decodes one of the two chunk groups
+// and hands its fragments to the other through a 32 KiB LDS exchange buffer (one 16-byte
+// store and one load per fragment), so every weight is decoded once per workgroup.  The
+// decode of the next K-step runs between the current step's MFMAs, one weight pair per
+// group of four MFMAs.  A reaches LDS by direct-to-LDS loads (no registers, no LDS store
+// instructions) two K-steps ahead, in three buffers.
+
+// A masked codebook word with the multiply-add in plain code for states off a half-word
+// boundary: the compiler schedules and renames it freely (v_mul_lo_u32 + v_add_u32), where
+// the single-instruction v_mad_u64_u32 form -- inline assembly with a 64-bit result -- left
+// this kernel's register allocation spilling.
+template <int K, int CB, int Q>
+__device__ __forceinline__ uint32_t rb_word(const uint32_t (&w)[K + 1], const Dot2Consts& k)
+{
+    using P = StatePlan<K, Q>;
+    uint32_t x;
+    if constexpr (P::kind <= 1) {
+        x = dot2_raw<K, CB, Q>(w, k);
+    } else {
+        const uint32_t st = state_field<K, Q>(w);
+        x = CB == CB_MCG ? st * CBMCG_MUL : st * k.mul + CB3_ADD;   // k.mul: the multiplier in a VGPR
+    }
+    return (x & k.mask) ^ k.flip;
+}
+
+// One 8-row fragment of a chunk as fp16 weights (the reconstruct rounding) in input order:
+// positions q0 + 8m + {0, 1}, m = 0..3 -- q0 = 0: column c rows 0..7, 2: column c rows 8..15,
+// 4: column c + 8 rows 0..7, 6: column c + 8 rows 8..15 (sk_decode's o[q0 / 2]).
+template <int K, int CB, int Q0>
+__device__ __forceinline__ uint4 rb_frag(const uint32_t (&w)[K + 1], const Dot2Consts& kc)
+{
+    return uint4{sk_pair(rb_word<K, CB, Q0>(w, kc), rb_word<K, CB, Q0 + 1>(w, kc)),
+                 sk_pair(rb_word<K, CB, Q0 + 8>(w, kc), rb_word<K, CB, Q0 + 9>(w, kc)),
+                 sk_pair(rb_word<K, CB, Q0 + 16>(w, kc), rb_word<K, CB, Q0 + 17>(w, kc)),
+                 sk_pair(rb_word<K, CB, Q0 + 24>(w, kc), rb_word<K, CB, Q0 + 25>(w, kc))};
+}
+
+// The lane's K words of a chunk, always loaded: every wave issues the same number of loads
+// per step, which the step-end waits count on.  A column past the shard reads column 0's
+// words (sk_bcol) and is left as loaded -- its 128-output block lies wholly past the shard
+// and is never stored -- so nothing consumes the loaded registers before the decode does.
+template <int K>
+__device__ __forceinline__ void rb_load(uint32_t (&w)[K + 1], const uint32_t* __restrict__ p)
+{
+    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    int i = 0;
+#pragma unroll
+    for (; i + 4 <= K; i += 4) {
+        uint4 v;
+        __builtin_memcpy(&v, p + i, 16);
+        w[i + 1] = v.x; w[i + 2] = v.y; w[i + 3] = v.z; w[i + 4] = v.w;
+    }
+    if constexpr (K % 4 == 3) {
+        u32x3 v;
+        __builtin_memcpy(&v, p + i, 12);
+        w[i + 1] = v.x; w[i + 2] = v.y; w[i + 3] = v.z;
+    } else if constexpr (K % 4 == 2) {
+        u32x2 v;
+        __builtin_memcpy(&v, p + i, 8);
+        w[i + 1] = v.x; w[i + 2] = v.y;
+    } else if constexpr (K % 4 == 1) {
+        w[i + 1] = p[i];
+    }
+}
+
+// f(integral_constant<int, I>) for I = B .. E - 1, in order.
+template <int B, int E, class F>
+__device__ __forceinline__ void rb_static_for(F&& f)
+{
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        rb_static_for<B + 1, E>(f);
+    }
+}
+
+// s_waitcnt until at most v vector-memory operations are outstanding (gfx9 encoding; no wait
+// on the export and LDS/scalar counters).
+constexpr int rb_vmcnt(int v) { return (v & 15) | ((v >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+template <int K, int CB>
+__global__ __launch_bounds__(64 * SK_WAVES) __attribute__((amdgpu_waves_per_eu(SK_WPE, SK_WPE)))
+void gemm_rb_kernel(const SkArgs a)
+{
+    constexpr int BM = 256, MB = SkCfg<BM>::MB, NB = SkCfg<BM>::NB;
+    static_assert(NB == 4 && MB == 8 && SkCfg<BM>::WN == 4, "two chunk groups x two column halves per wave");
+    constexpr int NBL = K / 4 + (K % 4 ? 1 : 0);   // B load instructions per step
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    auto As = [&](int b) { return reinterpret_cast<const _Float16*>(lds) + sk_rb_as(b); };
+    uint4* const bx = reinterpret_cast<uint4*>(lds) + sk_rb_bx_base();
+
+    const int g = sk_logical(blockIdx.x, gridDim.x);
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int wm = wave / SkCfg<BM>::WN, wn = wave % SkCfg<BM>::WN;
+    const int partner = sk_rb_partner(wave);
+    const Dot2Consts kc = dot2_consts();
+    const int c = lane & 7;
+    const bool first_lane = c == 0;
+
+    // acc[mb][2 h + ch]: h = 0 the wave's own chunk group (g = wm), h = 1 its partner's
+    f32x4 acc[MB][NB];
+
+    const uint32_t lds_base = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(void __attribute__((address_space(3)))*)lds);
+    const long u_begin = sk_first(a, g), u_end = sk_first(a, g + 1);
+    long u = u_begin;
+    while (u < u_end) {
+        const SkPiece pc = sk_piece<BM>(a, u, u_end);
+        const int s0 = pc.s0, s1 = pc.s1;
+        const SkShard& S = a.sh[pc.si];
+        const int m0 = pc.m0, tc = pc.tc;
+        const int bcol = sk_bcol(sk_rb_btn(lane, pc.tn, wn, wm), tc);
+        // in registers: the assembly loads below clobber memory, which would reload these
+        const uint16_t* const Ah = S.Ah;
+        const uint32_t* const Bt = S.trellis;
+        const int last_row = a.rows - 1;
+        const long ic = a.ic;
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        // Direct-to-LDS load of A(s) into buffer b: 4 passes, this wave's 8 rows each (rows past
+        // the call's read the last row: in bounds, and their outputs are never stored).  Issued
+        // as inline assembly, so the compiler's wait insertion does not see these loads: it
+        // would otherwise wait for every direct-to-LDS load before any later LDS read (it
+        // cannot tell the buffers apart) -- the step-end waits order them instead.
+        auto dma_a = [&](int s, int b) {
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const int r = sk_rb_dma_row(p, wave, lane);
+                const int row = min(m0 + r, last_row);
+                const uint16_t* src = Ah + (long)row * ic + s * SK_KS + 8 * sk_rb_dma_chunk(p, wave, lane);
+                const uint32_t dst = lds_base + 2u * (uint32_t)(sk_rb_as(b) + (64 * p + 8 * wave) * SK_KS);
+                asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(dst)
+                             : "memory", "m0");
+            }
+        };
+        auto run_piece = [&](auto kk) {
+            constexpr int KK = decltype(kk)::value;
+            uint32_t wc[KK + 1], wx[KK + 1];     // words of the chunk decoded this step, of the next
+            uint4 own[4], nown[4], pf[4];        // fragment f = 2 ch + rh
+            auto load_b = [&](uint32_t (&w)[KK + 1], int s) {
+                rb_load<KK>(w, Bt + sk_b_word(sk_rb_bti(lane, s), tc, bcol, c, KK));
+            };
+            auto decode_put = [&](uint32_t (&w)[KK + 1], uint4 (&o)[4], int b) {
+                chunk_prev_dpp<KK>(w, first_lane);
+                o[0] = rb_frag<KK, CB, 0>(w, kc);
+                o[1] = rb_frag<KK, CB, 2>(w, kc);
+                o[2] = rb_frag<KK, CB, 4>(w, kc);
+                o[3] = rb_frag<KK, CB, 6>(w, kc);
+#pragma unroll
+                for (int f = 0; f < 4; f++) bx[sk_rb_bx(b, wave, f, lane)] = o[f];
+            };
+            // One K-step's MFMAs on A buffer b3 and fragments own / pf, with the decode of the
+            // next step's own fragments (from wc, stored to B buffer bo) spread between them:
+            // 16 MFMA groups (row half rh outer, row block mb inner: an accumulator's next
+            // MFMA comes 32 MFMAs later), each of 4 MFMAs, one A-fragment read two groups
+            // ahead, and one weight pair of the decode; a fragment is stored every 4 groups.
+            // The order is fixed by scheduling barriers between groups.
+            auto step_body = [&](int b3, int bo) {
+                const _Float16* as = As(b3);
+                auto frag = [&](int i) {
+                    return *reinterpret_cast<const f16x8*>(as + sk_rb_a_frag(wm, i % MB, lane, i / MB));
+                };
+                f16x8 af[3];
+                af[0] = frag(0);
+                af[1] = frag(1);
+                chunk_prev_dpp<KK>(wc, first_lane);
+                uint32_t pr[4];
+                rb_static_for<0, 2 * MB>([&](auto ic) {
+                    constexpr int I = decltype(ic)::value;
+                    constexpr int mb = I % MB, rh = I / MB, f = I / 4, m = I % 4;
+                    if constexpr (I + 2 < 2 * MB) af[(I + 2) % 3] = frag(I + 2);
+#pragma unroll
+                    for (int ch = 0; ch < 2; ch++)
+                        acc[mb][ch] = mfma16x16x32(af[I % 3], __builtin_bit_cast(f16x8, own[2 * ch + rh]), acc[mb][ch]);
+#pragma unroll
+                    for (int ch = 0; ch < 2; ch++)
+                        acc[mb][2 + ch] = mfma16x16x32(af[I % 3], __builtin_bit_cast(f16x8, pf[2 * ch + rh]),
+                                                       acc[mb][2 + ch]);
+                    pr[m] = sk_pair(rb_word<KK, CB, 2 * f + 8 * m>(wc, kc), rb_word<KK, CB, 2 * f + 8 * m + 1>(wc, kc));
+                    if constexpr (m == 3) {
+                        nown[f] = uint4{pr[0], pr[1], pr[2], pr[3]};
+                        bx[sk_rb_bx(bo, wave, f, lane)] = nown[f];
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                });
+            };
+
+            // Prologue: A(s0), A(s0 + 1) into A buffers 0, 1; the own fragments of s0 decoded
+            // and stored to B buffer 0; the words of s0 + 1 loaded.
+            dma_a(s0, 0);
+            dma_a(min(s0 + 1, s1 - 1), 1);
+            load_b(wx, s0);
+            load_b(wc, min(s0 + 1, s1 - 1));
+            __builtin_amdgcn_s_waitcnt(rb_vmcnt(0));
+            decode_put(wx, own, 0);
+            __syncthreads();
+            // Step s: A(s + 2) streams into A buffer (s - s0 + 2) % 3 (last read at step s - 1)
+            // and the words of s + 2 into wx; the partner's fragments of s come from B buffer
+            // (s - s0) % 2, and this wave's fragments of s + 1 are decoded from wc and stored to
+            // the other B buffer (last read at step s - 1) while the MFMAs of s run.  Steps past
+            // the piece load and decode in-bounds data that is never used.
+            for (int s = s0; s < s1; s++) {
+                const int b3 = (s - s0) % SK_RB_NBUF, b2 = (s - s0) & 1;
+                dma_a(min(s + 2, s1 - 1), (s - s0 + 2) % SK_RB_NBUF);
+                load_b(wx, min(s + 2, s1 - 1));
+#pragma unroll
+                for (int f = 0; f < 4; f++) pf[f] = bx[sk_rb_bx(b2, partner, f, lane)];
+                step_body(b3, b2 ^ 1);
+                // A(s + 1) landed (only this step's loads may still be in flight)
+                __builtin_amdgcn_s_waitcnt(rb_vmcnt(4 + NBL));
+                __syncthreads();
+#pragma unroll
+                for (int f = 0; f < 4; f++) own[f] = nown[f];
+#pragma unroll
+                for (int i = 0; i <= KK; i++) wc[i] = wx[i];
+            }
+            __builtin_amdgcn_s_waitcnt(rb_vmcnt(0));       // no load still writing LDS
+        };
+        run_piece(std::integral_constant<int, K>{});
+        u += s1 - s0;
+        if (wm) {   // accumulator blocks in chunk-group order for the epilogue
 #pragma unroll
             for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-                for (int nb = 0; nb < NB; nb++) {
-                    const f32x4 v = acc[mb][nb];
-                    __hip_atomic_store(my + (long)((mb * NB + nb) * 2) * 64, sk_pack2(v.x, v.y), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                    __hip_atomic_store(my + (long)((mb * NB + nb) * 2 + 1) * 64, sk_pack2(v.z, v.w), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                for (int ch = 0; ch < 2; ch++) {
+                    const f32x4 t = acc[mb][ch];
+                    acc[mb][ch] = acc[mb][2 + ch];
+                    acc[mb][2 + ch] = t;
                 }
-            __builtin_amdgcn_s_waitcnt(0);   // this wave's slot stores are complete
-            __syncthreads();                  // ... and every wave's
-            if (tid == 0) {
-                const uint32_t old = __hip_atomic_fetch_add(a.counters + t, 1u, __ATOMIC_RELAXED,
-                                                            __HIP_MEMORY_SCOPE_AGENT);
-                lds[0] = old == (uint32_t)(g_hi - g_lo) ? 1u : 0u;
-            }
-            __syncthreads();
-            finish = lds[0] != 0u;
-            __syncthreads();                  // lds[0] read by all before LDS is reused
-            if (finish) {
-                // last to arrive: every contributor's stores completed before its increment
-#pragma unroll
-                for (int mb = 0; mb < MB; mb++)
-#pragma unroll
-                    for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-                // Slots in workgroup order, each read in batches of SK_RB 8-byte loads per lane
-                // that are all issued before the first add (atomic loads keep program order,
-                // so loads interleaved with the adds would have two in flight at a time).
-                constexpr int NP = MB * NB * 2;                   // 8-byte words per lane and slot
-                constexpr int RB = NP < 16 ? NP : 16;
-                for (int gg = g_lo; gg <= g_hi; gg++) {
-                    const uint64_t* sl =
-                        reinterpret_cast<const uint64_t*>(a.slots + sk_slot<BM>(t, gg, wave)) + lane;
-#pragma unroll
-                    for (int b0 = 0; b0 < NP; b0 += RB) {
-                        uint64_t v[RB];
-#pragma unroll
-                        for (int i = 0; i < RB; i++)
-                            v[i] = __hip_atomic_load(sl + (long)(b0 + i) * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-                        for (int i = 0; i < RB; i += 2) {
-                            const int blk = (b0 + i) >> 1, mb = blk / NB, nb = blk % NB;
-                            acc[mb][nb] += f32x4{__builtin_bit_cast(float, (uint32_t)v[i]),
-                                                 __builtin_bit_cast(float, (uint32_t)(v[i] >> 32)),
-                                                 __builtin_bit_cast(float, (uint32_t)v[i + 1]),
-                                                 __builtin_bit_cast(float, (uint32_t)(v[i + 1] >> 32))};
-                        }
-                    }
-                }
-            }
         }
-        if (finish) {
-            // svh pair of this lane in the 128-output block starting at tile column ob, read
-            // once per block: the fp16 output stores could alias it, so a load inside the
-            // row loop would be repeated (a round trip per row)
-            auto load_sv = [&](int ob) -> uint32_t {
-                return ob < tc ? reinterpret_cast<const uint32_t*>(S.svh + ob * 16)[lane] : 0u;
-            };
-            auto store_row = [&](int row, int ob, uint32_t sv, float v0, float v1) {
-                // ob: tile column of the 128-output block's first output
-                wave_fwht128(v0, v1);
-                if (ob < tc && row < a.rows) {
-                    const float sv0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv & 0xffffu));
-                    const float sv1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sv >> 16));
-                    const uint32_t o = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v0 * sv0)) |
-                                       ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(v1 * sv1)) << 16);
-                    reinterpret_cast<uint32_t*>(S.C + (long)row * S.ldc + ob * 16)[lane] = o;
-                }
-            };
-            __syncthreads();                  // every wave is done with the A/B tiles
-            if constexpr (BM == 256) {
-                // Output block of rows 128 wm ..: waves wn = 2 blk and 2 blk + 1 hold its two
-                // 64-column halves.  16 rows at a time through LDS (16 x 132 floats per block
-                // and row half), then wave (wn & 1) transforms rows 8 (wn & 1) .. + 7.
-                const int blk = wn >> 1, half = wn & 1;
-                const uint32_t sv = load_sv(16 * tn + 8 * blk);
-                float* cs = reinterpret_cast<float*>(lds) + sk_c256(wm, blk, 0, 0);
-#pragma unroll
-                for (int mb = 0; mb < MB; mb++) {
-#pragma unroll
-                    for (int nb = 0; nb < NB; nb++)
-#pragma unroll
-                        for (int e = 0; e < 4; e++)
-                            cs[sk_c256(0, 0, 4 * (lane >> 4) + e, 64 * half + 16 * nb + (lane & 15))] = acc[mb][nb][e];
-                    __syncthreads();
-#pragma unroll
-                    for (int r = 8 * half; r < 8 * half + 8; r++)   // eight independent transforms
-                        store_row(m0 + 128 * wm + 16 * mb + r, 16 * tn + 8 * blk, sv, cs[sk_c256(0, 0, r, 2 * lane)],
-                                  cs[sk_c256(0, 0, r, 2 * lane + 1)]);
-                    __syncthreads();
-                }
-            } else {
-                // 16 rows at a time through LDS (16 rows of 260 floats); wave w transforms the
-                // chunk's (row, block) pairs w, w + 8, w + 16, w + 24
-                float* cs = reinterpret_cast<float*>(lds);
-                const uint32_t sv[2] = {load_sv(16 * tn), load_sv(16 * tn + 8)};
-#pragma unroll
-                for (int mb = 0; mb < MB; mb++) {
-#pragma unroll
-                    for (int nb = 0; nb < NB; nb++)
-#pragma unroll
-                        for (int e = 0; e < 4; e++)
-                            cs[sk_cx(4 * (lane >> 4) + e, NB * 16 * wn + 16 * nb + (lane & 15))] = acc[mb][nb][e];
-                    __syncthreads();
-#pragma unroll
-                    for (int jj = 0; jj < 4; jj++) {
-                        const int j = wave + SK_WAVES * jj;
-                        const int r = j & 15, blk = j >> 4;
-                        store_row(m0 + 16 * mb + r, 16 * tn + 8 * blk, sv[blk], cs[sk_cx(r, 128 * blk + 2 * lane)],
-                                  cs[sk_cx(r, 128 * blk + 2 * lane + 1)]);
-                    }
-                    if (mb + 1 < MB) __syncthreads();
-                }
-            }
-        }
-        __syncthreads();                      // LDS is free for the next piece
+        sk_finish_piece<BM, true>(a, pc, S, g, wave, lane, tid, wm, wn, acc, lds);
     }
 }
 
@@ -399,8 +708,24 @@ size_t gemm_grouped_shard_bytes(int rows, int ic, int oc)
     return sk_grouped_bytes_bm(gemm_sk_bm(rows), rows, ic, oc, gemm_sk_cus());
 }
 
+// The 256-row form is the register-B kernel (ORCA_EXL3_SK_RB=0 selects the LDS-B kernel of
+// the other tile heights at 256 rows, for comparison).
+static bool sk_use_rb()
+{
+    static const bool rb = [] {
+        const char* e = getenv("ORCA_EXL3_SK_RB");
+        return !(e && e[0] == '0');
+    }();
+    return rb;
+}
+
 template <int K, int CB, int BM>
-static const void* sk_fn() { return reinterpret_cast<const void*>(&gemm_sk_kernel<K, CB, BM>); }
+static const void* sk_fn()
+{
+    if constexpr (sk_rb<BM>() && K > 0)
+        if (sk_use_rb()) return reinterpret_cast<const void*>(&gemm_rb_kernel<K, CB>);
+    return reinterpret_cast<const void*>(&gemm_sk_kernel<K, CB, BM>);
+}
 
 template <int BM>
 static const void* sk_fn_kcb(int K, int cb)
@@ -437,7 +762,7 @@ static int sk_lds_any(int BM)
     case 64: return sk_lds<64>();
     case 96: return sk_lds<96>();
     case 128: return sk_lds<128>();
-    default: return sk_lds<256>();
+    default: return sk_use_rb() ? sk_rb_lds() : sk_lds<256>();
     }
 }
 

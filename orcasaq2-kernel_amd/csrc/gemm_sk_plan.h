@@ -194,6 +194,54 @@ SK_HD int sk_a_frag(int wm, int mb, int lane, int h)
     return (SkCfg<BM>::MB * 16 * wm + 16 * mb + (lane & 15)) * SK_LD + 32 * h + 8 * (lane >> 4);
 }
 
+// ---------------------------------------------------------------- 256-row tiles: B in registers
+//
+// The 256-row form (gemm_rb_kernel) keeps only A in LDS (below).
+// Each wave (wm, wn) owns rows 128 wm .. and outputs 64 wn .. of the tile: two chunk groups g
+// of 32 outputs (two tile columns).  Per K-step lane l of the wave decodes one chunk of group
+// g = wm -- chunk l % 8 of tile (4 s + l / 16, 16 tn + 4 wn + 2 g + (l % 16) / 8) -- and
+// receives lane l's chunk of group 1 - wm from wave (1 - wm, wn); a chunk's four 8-row
+// fragments (column half ch, row half rh) are the B operands of four
+// v_mfma_f32_16x16x32_f16: the MFMA's k-group j = l / 16 is tile row 4 s + j, rows 8 rh ..
+// 8 rh + 7, and its column n = l % 16 is output 16 (n / 8) + 8 ch + n % 8 of the group.  The
+// A operand of row block mb and half rh: row 16 mb + l % 16 of the wave's 128, inputs
+// 16 (l / 16) + 8 rh .. + 7 of the K-step.  Accumulator block nb = 2 g + ch.
+template <int BM>
+constexpr bool sk_rb() { return BM == 256; }
+SK_HD int sk_rb_bti(int lane, int s) { return 4 * s + (lane >> 4); }
+SK_HD int sk_rb_btn(int lane, int tn, int wn, int g) { return 16 * tn + 4 * wn + 2 * g + ((lane & 15) >> 3); }
+// A tiles: SK_RB_NBUF buffers of 256 rows x 64 halves, unpadded; a row's eight 16-byte chunks
+// are stored XOR-swizzled (logical chunk c of row r at chunk c ^ ((r / 2) % 8)).  A row is
+// half of a 256-byte bank line, so the 16 rows of an MFMA fragment read (one logical chunk
+// each) fall on 16 distinct 16-byte bank groups -- rows of equal parity are told apart by
+// (r / 2) % 8 -- while each wave's 16-byte direct-to-LDS loads fill 8 whole rows (1 KiB) in
+// lane order.
+constexpr int SK_RB_NBUF = 3;
+SK_HD int sk_rb_as(int b) { return b * 256 * SK_KS; }
+SK_HD int sk_rb_chunk_swz(int r) { return (r >> 1) & 7; }
+SK_HD int sk_rb_swz(int r, int c) { return r * SK_KS + 8 * (c ^ sk_rb_chunk_swz(r)); }
+SK_HD int sk_rb_a_frag(int wm, int mb, int lane, int rh)
+{
+    return sk_rb_swz(128 * wm + 16 * mb + (lane & 15), 2 * (lane >> 4) + rh);
+}
+// Direct load of pass p (0..3) by wave wv: LDS rows 64 p + 8 wv .. + 7 in lane order; lane l
+// fills chunk l % 8 of row 64 p + 8 wv + l / 8, i.e. logical chunk (l % 8) ^ ((row / 2) % 8).
+SK_HD int sk_rb_dma_row(int p, int wv, int lane) { return 64 * p + 8 * wv + (lane >> 3); }
+SK_HD int sk_rb_dma_chunk(int p, int wv, int lane) { return (lane & 7) ^ sk_rb_chunk_swz(sk_rb_dma_row(p, wv, lane)); }
+// Output (0..63 within the wave's 64) of accumulator block nb, lane's column.
+SK_HD int sk_rb_wcol(int nb, int lane)
+{
+    return 32 * (nb >> 1) + 16 * ((lane & 15) >> 3) + 8 * (nb & 1) + (lane & 7);
+}
+// B fragment exchange: two buffers (K-step parity) after the A buffers, each 8 waves x 4
+// fragments x 64 lanes of 16 bytes; a wave stores its own chunk group's fragments in lane
+// order and reads its partner's (conflict-free 16-byte accesses).  Partner of (wm, wn): (1 - wm, wn).
+constexpr int SK_RB_BBUF = 2;
+SK_HD int sk_rb_partner(int wave) { return wave ^ 4; }
+SK_HD int sk_rb_bx_base() { return SK_RB_NBUF * 256 * SK_KS * 2 / 16; }   // in 16-byte units
+SK_HD int sk_rb_bx(int b, int wave, int f, int lane) { return ((b * SK_WAVES + wave) * 4 + f) * 64 + lane; }
+constexpr int sk_rb_lds() { return SK_RB_NBUF * 256 * SK_KS * 2 + SK_RB_BBUF * SK_WAVES * 4 * 64 * 16; }   // bytes
+
 // Slot of (tile t, workgroup g, wave): float offset of its acc x 64 partials; the lane's
 // 8-byte word i of it is u64 i * 64 + lane.
 template <int BM>

@@ -14,9 +14,11 @@
 // Nothing here runs on a GPU; the library is built with hipcc only because the shared index
 // functions are marked __host__ __device__.
 #include <stdarg.h>
+#include <stdlib.h>
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <string>
 #include <vector>
@@ -554,6 +556,98 @@ void sk_check_lds()
     }
 }
 
+// Whether a BM-row launch of K bits runs the register-B kernel (gemm_sk.hip's sk_fn and
+// sk_use_rb: 256-row tiles of one bit width, unless ORCA_EXL3_SK_RB=0).
+template <int BM>
+bool sk_replay_rb(int K)
+{
+    const char* e = getenv("ORCA_EXL3_SK_RB");
+    return sk_rb<BM>() && K > 0 && !(e && e[0] == '0');
+}
+
+// The register-B kernel's LDS: three A buffers filled by direct-to-LDS loads (each logical
+// (row, 16-byte chunk) of a K-step's 256 x 64 tile lands once, where the fragment reads look
+// for it), the two fragment-exchange buffers (each wave's stores read back by its partner
+// only, same fragment and lane), and the epilogue staging with the register-B column map.
+void sk_check_lds_rb()
+{
+    const int lds_bytes = sk_rb_lds();
+    const int a_halves = sk_rb_as(SK_RB_NBUF);
+    for (int b = 0; b < SK_RB_NBUF; b++) {
+        std::vector<int> who((size_t)256 * SK_KS / 8, -1);   // physical chunk -> logical row * 8 + chunk
+        for (int wave = 0; wave < SK_WAVES; wave++)
+            for (int p = 0; p < 4; p++)
+                for (int lane = 0; lane < 64; lane++) {
+                    // the DMA writes lane l's 16 bytes at the pass base + 16 l
+                    const int h = sk_rb_as(b) + (64 * p + 8 * wave) * SK_KS + 8 * lane;
+                    if (h < sk_rb_as(b) || h + 8 > sk_rb_as(b + 1)) fail("A load into LDS outside buffer %d", b);
+                    const int r = sk_rb_dma_row(p, wave, lane), c = sk_rb_dma_chunk(p, wave, lane);
+                    if (r < 0 || r >= 256 || c < 0 || c >= 8) fail("A load of row %d chunk %d", r, c);
+                    if (sk_rb_as(b) + sk_rb_swz(r, c) != h) fail("A row %d chunk %d lands where reads do not look", r, c);
+                    int& w = who[(h - sk_rb_as(b)) / 8];
+                    if (w >= 0) fail("A buffer %d chunk %d written twice", b, (h - sk_rb_as(b)) / 8);
+                    w = r * 8 + c;
+                }
+        for (size_t i = 0; i < who.size(); i++)
+            if (who[i] < 0) fail("A buffer %d chunk %zu never written", b, i);
+        for (int wave = 0; wave < SK_WAVES; wave++) {
+            const int wm = wave / SkCfg<256>::WN;
+            for (int lane = 0; lane < 64; lane++)
+                for (int mb = 0; mb < SkCfg<256>::MB; mb++)
+                    for (int rh = 0; rh < 2; rh++) {
+                        const int h = sk_rb_a_frag(wm, mb, lane, rh);
+                        if (h < 0 || h % 8 || h + 8 > 256 * SK_KS) fail("A fragment read outside the tile");
+                        const int row = 128 * wm + 16 * mb + (lane & 15), chunk = 2 * (lane >> 4) + rh;
+                        if (who[h / 8] != row * 8 + chunk) fail("A fragment (row %d, chunk %d) reads another chunk", row, chunk);
+                    }
+        }
+    }
+    // exchange buffers: after the A buffers, inside the launch's LDS
+    if (sk_rb_bx_base() * 16 < a_halves * 2) fail("exchange buffers overlap the A buffers");
+    std::vector<int> xw((size_t)SK_RB_BBUF * SK_WAVES * 4 * 64, -1);
+    for (int b = 0; b < SK_RB_BBUF; b++)
+        for (int wave = 0; wave < SK_WAVES; wave++)
+            for (int f = 0; f < 4; f++)
+                for (int lane = 0; lane < 64; lane++) {
+                    const int i = sk_rb_bx(b, wave, f, lane);
+                    if (i < 0 || (size_t)i >= xw.size() || (sk_rb_bx_base() + i + 1) * 16 > lds_bytes)
+                        fail("fragment store outside the exchange buffers");
+                    if (xw[i] >= 0) fail("exchange slot %d stored twice", i);
+                    xw[i] = ((b * SK_WAVES + wave) * 4 + f) * 64 + lane;
+                }
+    for (int b = 0; b < SK_RB_BBUF; b++)
+        for (int wave = 0; wave < SK_WAVES; wave++) {
+            const int pw = sk_rb_partner(wave);
+            if (pw == wave || sk_rb_partner(pw) != wave || pw % SkCfg<256>::WN != wave % SkCfg<256>::WN)
+                fail("wave %d: partner %d does not share its outputs", wave, pw);
+            for (int f = 0; f < 4; f++)
+                for (int lane = 0; lane < 64; lane++)
+                    if (xw[sk_rb_bx(b, pw, f, lane)] != ((b * SK_WAVES + pw) * 4 + f) * 64 + lane)
+                        fail("wave %d reads another fragment than its partner stored", wave);
+        }
+    // epilogue staging (register-B column map): per output block and row half, every element
+    // of the 16 x 128 staging rows written once by the block's two waves
+    const int lds_floats = lds_bytes / 4;
+    for (int wm = 0; wm < 2; wm++)
+        for (int blk = 0; blk < 2; blk++) {
+            std::vector<int> cnt(16 * 128, 0);
+            for (int half = 0; half < 2; half++) {
+                const int wn = 2 * blk + half;
+                for (int lane = 0; lane < 64; lane++)
+                    for (int nb = 0; nb < SkCfg<256>::NB; nb++)
+                        for (int e = 0; e < 4; e++) {
+                            const int row = 4 * (lane >> 4) + e, col = 64 * half + sk_rb_wcol(nb, lane);
+                            if (col < 0 || col >= 128) fail("staging column %d", col);
+                            const int i = sk_c256(wm, blk, row, col);
+                            if (i < 0 || i >= lds_floats) fail("epilogue staging store beyond LDS (register-B)");
+                            cnt[row * 128 + col]++;
+                        }
+            }
+            for (int i = 0; i < 16 * 128; i++)
+                if (cnt[i] != 1) fail("staging (wm %d, block %d) element %d written %d times", wm, blk, i, cnt[i]);
+        }
+}
+
 // One BM-row launch (after the clear or set-up kernel): every workgroup's pieces, their loads,
 // slot traffic and epilogue stores.
 template <int BM>
@@ -566,7 +660,9 @@ void sk_replay_launch(SkWorld& W, const GemvShard* shards, const SkLaunch& L, in
     if (G < 1) fail("launch %d: %d workgroups", launch, G);
     if (sk_first(a, G) != units) fail("launch %d: ranges end at %ld, not %ld", launch, sk_first(a, G), units);
     if (a.q < 1) fail("launch %d: %d K-steps per workgroup", launch, a.q);
-    sk_check_lds<BM>();
+    const bool rb = sk_replay_rb<BM>(L.K);
+    if (rb) sk_check_lds_rb();
+    else sk_check_lds<BM>();
     // counters and slots inside the workspace share of this launch
     ws_region(W, a.counters, (long)a.ntiles * 4, "tile counters");
     const long slot_floats = (long)(a.ntiles + G) * SK_WAVES * sk_acc<BM>() * 64;
@@ -636,8 +732,52 @@ void sk_replay_launch(SkWorld& W, const GemvShard* shards, const SkLaunch& L, in
             const int KK = L.K > 0 ? L.K : S.K;
             if (KK != W.sh[gi].K) fail("piece decodes K=%d, shard has K=%d", KK, W.sh[gi].K);
             const long twords = (long)(W.sh[gi].ic / 16) * (W.sh[gi].oc / 16) * 8 * KK;
+            auto load_step_rb = [&](int s) {
+                // direct-to-LDS A loads (rows past the call's read the last row) and every lane's
+                // chunk words (a column past the shard reads column 0); each chunk of the
+                // K-step's tile rows and the piece's 16 tile columns decoded by one lane
+                std::vector<uint8_t> dec(4 * 16 * 8, 0);
+                for (int wave = 0; wave < SK_WAVES; wave++) {
+                    const int wm = wave / SkCfg<256>::WN, wn = wave % SkCfg<256>::WN;
+                    for (int lane = 0; lane < 64; lane++) {
+                        for (int p = 0; p < 4; p++) {
+                            const int row = std::min(pc.m0 + sk_rb_dma_row(p, wave, lane), a.rows - 1);
+                            const long el = (long)row * a.ic + (long)s * SK_KS + 8 * sk_rb_dma_chunk(p, wave, lane);
+                            need_in(S.Ah + el, 16, W.ah_buf[gi] >= 0 ? W.ah_buf[gi] : B_WS,
+                                    W.ah_buf[gi] >= 0 ? (long)a.rows * a.ic * 2 : (long)W.ws_bytes, "A tile load");
+                            if (el / a.ic != row || el % a.ic < (long)s * SK_KS || el % a.ic + 8 > (long)(s + 1) * SK_KS)
+                                fail("A tile load of row %d K-step %d reads row %ld column %ld", row, s, el / a.ic, el % a.ic);
+                        }
+                        const int btn = sk_rb_btn(lane, pc.tn, wn, wm);
+                        const long wd = sk_b_word(sk_rb_bti(lane, s), pc.tc, sk_bcol(btn, pc.tc), lane & 7, KK);
+                        need_in(S.trellis + wd, 4L * KK, B_TRELLIS + gi, twords * 4, "trellis load");
+                        const long tile = wd / (8 * KK), ti = tile / pc.tc, tj = tile % pc.tc;
+                        if (ti != 4L * s + (lane >> 4) || wd % (8 * KK) != (long)(lane & 7) * KK)
+                            fail("trellis load of K-step %d lane %d reads tile row %ld", s, lane, ti);
+                        if (btn < pc.tc) {
+                            if (tj != btn) fail("trellis load of column %d reads column %ld", btn, tj);
+                            if (btn < 16 * pc.tn || btn >= 16 * pc.tn + 16) fail("column %d outside block %d", btn, pc.tn);
+                            dec[((lane >> 4) * 16 + (btn - 16 * pc.tn)) * 8 + (lane & 7)]++;
+                        } else if (tj != 0) {
+                            fail("trellis load past the shard reads column %ld, not 0", tj);
+                        }
+                    }
+                }
+                for (int tr = 0; tr < 4; tr++)
+                    for (int j = 0; j < 16; j++)
+                        for (int c = 0; c < 8; c++) {
+                            const int n = dec[(tr * 16 + j) * 8 + c];
+                            if (n != (16 * pc.tn + j < pc.tc ? 1 : 0))
+                                fail("K-step %d chunk (%d, %d, %d) decoded %d times", s, tr, j, c, n);
+                        }
+            };
             auto load_step = [&](int s) {
                 if (s < pc.s0 || s >= pc.s1) fail("K-step %d loaded outside the piece %d..%d", s, pc.s0, pc.s1);
+                if (rb) {
+                    load_step_rb(s);
+                    W.loads++;
+                    return;
+                }
                 for (int tid = 0; tid < 64 * SK_WAVES; tid++) {
                     const int arow = sk_arow(tid), aseg = sk_aseg(tid);
                     for (int p = 0; p < AP; p++) {
