@@ -14,7 +14,7 @@ replays its steps), so host launch overhead is not part of the measurement; the
 warm-up steps are a graph replay too.
 `value` = total packed trellis bytes / total time over the timed steps.
 `roofline` = the dominant GEMV (the K whose call moves the most bytes; one call = one
-gemv1_kernel<K> launch and one gemv1_finish_kernel launch): algorithmic bytes per call
+gemv1_kernel<K> launch, which also finishes its split column groups): algorithmic bytes per call
 (ic*oc*K/8) / its mean duration from HIP events recorded on the replay stream around a
 graph of the same steps, against 8 TB/s.  `traffic` = HBM bytes per call measured with
 rocprofv3 FETCH_SIZE + WRITE_SIZE and scaled by the same counters' reading for a plain
@@ -170,15 +170,9 @@ def gpu_bench(args) -> dict:
 
 
 def _rand_linear(ic, oc, K, g, dev):
-    """One synthetic EXL3 tensor set made on the GPU (same distributions as
-    orcasaq2.synthetic: uniform 16-bit trellis words, +-1 suh, +-|N(0,1)|/sqrt(ic) svh)."""
-    import torch
-    t = torch.randint(-32768, 32768, (ic // 16, oc // 16, 16 * K), generator=g, device=dev,
-                      dtype=torch.int32).to(torch.int16)
-    suh = (torch.randint(0, 2, (ic,), generator=g, device=dev) * 2 - 1).half()
-    svh = ((torch.randn(oc, generator=g, device=dev).abs() / math.sqrt(ic)).half()
-           * (torch.randint(0, 2, (oc,), generator=g, device=dev) * 2 - 1).half())
-    return dict(trellis=t, suh=suh, svh=svh, oc=oc, K=K, codebook=0)
+    """One synthetic EXL3 tensor set made on the GPU (orcasaq2.synthetic.linear_gpu)."""
+    from orcasaq2 import synthetic as syn
+    return syn.linear_gpu(ic, oc, K, g, dev)
 
 
 def _graph(dev, fn, settle=True):
@@ -262,9 +256,6 @@ def prefill_bench(reps: int) -> dict:
     return out
 
 
-CODEBOOK_RMS = 1.2437   # RMS of the 3INST codebook's 2^16 values
-
-
 def stack_bench(tokens: int = 20) -> dict:
     """Config 4: the linear stack of a 64-layer Qwen-27B-shaped decoder at batch-1 decode,
     one token = the int8 embedding gather, per layer the grouped q/k/v GEMV, o_proj, the
@@ -273,34 +264,17 @@ def stack_bench(tokens: int = 20) -> dict:
     but every projection reads what the one before it produced, so
     nothing runs before its input exists: o_proj reads the q columns of qkv (the width of
     the attention output it stands for), gate/up read o_proj's output, down_proj reads the
-    gate columns, the next layer reads down_proj's output, the lm_head the last one.  The
-    svh scales are |N(0,1)|/sqrt(ic)/CODEBOOK_RMS so each projection keeps the activation
-    RMS and 257 chained projections stay finite in fp16.  The token is captured once into
-    a HIP graph and replayed `tokens` times."""
+    gate columns, the next layer reads down_proj's output, the lm_head the last one
+    (orcasaq2.synthetic.stack_gpu builds the tensors).  The token is captured once into a
+    HIP graph and replayed `tokens` times."""
     import torch
     from orcasaq2 import _native
     from orcasaq2 import synthetic as syn
 
     dev = torch.device("cuda", 0)
-    g = torch.Generator(device=dev).manual_seed(4)
-    shapes = syn.stack_shapes()
-    layers = []
-    nbytes = 0
-
-    def lin(ic, oc, K):
-        d = _rand_linear(ic, oc, K, g, dev)
-        d["svh"] = (d["svh"].float() / CODEBOOK_RMS).half()
-        return d
-
-    for bits in syn.stack_bits():
-        layers.append({n: lin(*shapes[n], bits[n]) for n in shapes})
-        nbytes += sum(syn.packed_bytes(*shapes[n], bits[n]) for n in shapes)
-    head = lin(syn.HIDDEN, syn.VOCAB, 6)
-    nbytes += syn.packed_bytes(syn.HIDDEN, syn.VOCAB, 6)
-    table = torch.randint(-128, 128, (syn.VOCAB, syn.HIDDEN), generator=g, device=dev, dtype=torch.int8)
-    scales = (torch.rand(syn.VOCAB, 1, generator=g, device=dev) * 0.02 + 0.001).half()
+    st = syn.stack_gpu(dev)
+    layers, head, table, scales, nbytes = st["layers"], st["head"], st["table"], st["scales"], st["nbytes"]
     ids = torch.tensor([12345], device=dev)
-    nbytes += syn.HIDDEN + 2
     y_qkv = torch.empty(1, syn.Q_OUT + 2 * syn.KV_OUT, dtype=torch.half, device=dev)
     y_o = torch.empty(1, syn.HIDDEN, dtype=torch.half, device=dev)
     y_gu = torch.empty(1, 2 * syn.INTERMEDIATE, dtype=torch.half, device=dev)
@@ -719,8 +693,8 @@ def main():
                    "hbm_frac": round(r["value"] / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(dom["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(dom["frac"], 4), "traffic": traffic,
-                     "kernel": f"exl3_gemv K={r['dom']}: gemv1_kernel<{r['dom']}, 0, true, 1> + gemv1_finish_kernel<1, true> "
-                               "(one call = the decode launch and the launch that adds the split column groups)",
+                     "kernel": f"exl3_gemv K={r['dom']}: gemv1_kernel<{r['dom']}, 0, true, 1> (one call = one decode "
+                               "launch; its split column groups are finished inside it)",
                      "bytes_per_launch": dom["bytes"], "mean_launch_us": round(dom["mean_us"], 3)},
         "per_K": {str(K): {"GB/s": round(v["gbs"], 1), "frac": round(v["frac"], 4),
                            "mean_us": round(v["mean_us"], 3)} for K, v in r["per_k"].items()},

@@ -19,10 +19,12 @@
  *     as EXL3_ERR_UNSUPPORTED.
  *   - Workspaces are caller-owned device buffers (256-byte aligned) of at least the
  *     *_workspace_bytes() size; a call uses its workspace until its last kernel has run,
- *     so calls that may overlap in time must not share one.  Workspaces have no required
- *     contents (a GEMV workspace starts with a reserved 16 KiB area that no call reads),
- *     so one buffer serves any sequence of calls issued in order on one stream -- also
- *     HIP-graph replays of captured calls.
+ *     so calls that may overlap in time must not share one.  GEMM and top-k workspaces
+ *     have no required contents.  A GEMV workspace is a reserved 16 KiB head (no call
+ *     reads it), then EXL3_GEMV_ACC_BYTES of accumulators that must be zero-filled before
+ *     the workspace's first call -- every call leaves them zero-filled again -- then
+ *     scratch with no required contents.  So one buffer serves any sequence of calls
+ *     issued in order on one stream -- also HIP-graph replays of captured calls.
  */
 #ifndef EXL3HIP_H
 #define EXL3HIP_H
@@ -45,6 +47,8 @@ extern "C" {
 #define EXL3_CB_MUL1 2
 
 #define EXL3_GEMV_MAX_ROWS 16
+/* Zero-filled accumulator area at byte 16384 of every GEMV workspace (see above). */
+#define EXL3_GEMV_ACC_BYTES (2u << 20)
 #define EXL3_MAX_SHARDS 64
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -56,8 +60,10 @@ int exl3_abi_version(void);
 /*
  * Capture state of `stream`: *id = 0 when the stream is not being captured into a HIP
  * graph, else the capture's unique id (hipStreamGetCaptureInfo).  No counterpart in the
- * reference: the Python layer keys its GEMV workspaces by capture, so that a workspace
- * whose zero-fill was recorded into one graph is never used outside it.  Host-only.
+ * reference: the Python layer keys its GEMV workspaces by capture.  A workspace made during
+ * a capture comes from that graph's private memory pool, and its zero-fill is a node of
+ * that graph that runs only when the graph replays, so it is never used outside it.
+ * Host-only.
  */
 int exl3_stream_capture_id(void* stream, unsigned long long* id);
 
@@ -91,10 +97,13 @@ int exl3_had_r_128(const void* in, void* out, const void* pre, const void* post,
  *   C (rows, oc) = fp16( H( fp16(H(A * suh)) . W_q ) * svh ),  A (rows, ic) fp16.
  * Replaces ext.exl3_gemm(A, trellis, C, suh, A_had, svh, -1, mcg, mul1, 0)
  * [orcasaq2/ops.py:46-49] for rows <= 16 (the A_had scratch is internal to the kernel).
- * rows 1..4 take one decode launch per codebook (followed, when a column group's inputs
- * were split over several workgroups, by one small kernel that adds the split partial
- * sums); 5..16 rows take a set-up kernel (every shard's transformed activations), then per
- * codebook one decode launch and one finishing launch.
+ * rows 1..4 take one decode launch per codebook: a column group whose inputs are split over
+ * several workgroups is added up in the workspace's accumulators and finished by the
+ * workgroup that adds last (when a call's accumulators would exceed EXL3_GEMV_ACC_BYTES,
+ * one small kernel after the launch adds the split partial sums instead); 5..16 rows take a
+ * set-up kernel (every shard's transformed activations), then per codebook one decode
+ * launch and one finishing launch.  Results do not depend on the order workgroups finish
+ * in: the same inputs give the same bits on every call.
  */
 size_t exl3_gemv_workspace_bytes(int rows, int ic, int oc);
 int exl3_gemv(const void* A, const void* trellis, void* C, const void* suh, const void* svh,
@@ -129,14 +138,15 @@ int exl3_gemv_grouped(const void* A, const exl3_shard_t* shards, int nshards, vo
  * exl3_gemv_grouped without a workspace argument: it allocates nothing (no hipMalloc, no
  * library allocation), for callers that cannot allocate -- code under HIP-graph capture,
  * serving loops that forbid device allocation.  No counterpart in the reference.
- * The scratch is a file-scope device array of EXL3_STATIC_SCRATCH_BYTES (16 MiB), one per
- * GPU, held until the process ends; a call whose exl3_gemv_grouped_workspace_bytes exceeds
+ * The scratch is a file-scope device array of EXL3_STATIC_SCRATCH_BYTES (20 MiB), one per
+ * GPU (zero-filled when the library is loaded, as a GEMV workspace's accumulators must
+ * be), held until the process ends; a call whose exl3_gemv_grouped_workspace_bytes exceeds
  * it fails with EXL3_ERR_WORKSPACE (rows 1..4 fit every shape of the 27B model and its
  * 151936-wide lm_head; rows 5..16 fit every layer of that model and its lm_head).  All calls on one GPU
  * share the array and each leaves it ready for the next, so calls issued in order (one
  * stream, or graph replays in order) are safe; calls that may overlap in time race on it.
  */
-#define EXL3_STATIC_SCRATCH_BYTES (16u << 20)
+#define EXL3_STATIC_SCRATCH_BYTES (20u << 20)
 int exl3_gemv_grouped_static(const void* A, const exl3_shard_t* shards, int nshards, int rows, int ic,
                              void* stream);
 

@@ -84,7 +84,7 @@ extern "C" {
 
 const char* exl3_last_error(void) { return g_err; }
 
-int exl3_abi_version(void) { return 6; }
+int exl3_abi_version(void) { return 7; }
 
 int exl3_stream_capture_id(void* stream, unsigned long long* id)
 {
@@ -147,13 +147,13 @@ int exl3_had_r_128(const void* in, void* out, const void* pre, const void* post,
 size_t exl3_gemv_workspace_bytes(int rows, int ic, int oc)
 {
     if (rows < 1 || ic < 128 || oc < 128) return 0;
-    return GEMV_COUNTER_BYTES + gemv_workspace_bytes(rows, ic, oc);
+    return GEMV_COUNTER_BYTES + GEMV_ACC_BYTES + gemv_workspace_bytes(rows, ic, oc);
 }
 
 size_t exl3_gemv_grouped_workspace_bytes(const exl3_shard_t* shards, int nshards, int rows, int ic)
 {
     if (!shards || nshards < 1 || rows < 1 || ic < 128) return 0;
-    size_t t = GEMV_COUNTER_BYTES;
+    size_t t = GEMV_COUNTER_BYTES + GEMV_ACC_BYTES;
     for (int i = 0; i < nshards; i++) {
         if (shards[i].oc < 128) return 0;
         t += gemv_workspace_bytes(rows, ic, shards[i].oc);

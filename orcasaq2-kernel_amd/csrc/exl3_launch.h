@@ -35,16 +35,18 @@ struct GemvShard {
     long ldc;
 };
 
-// A reserved 16 KiB area at the head of every GEMV workspace (no kernel reads or writes it;
-// it keeps the published workspace layout and sizes).  The partial-sum buffers of all GEMV
-// paths start after it.
+// A GEMV workspace: a reserved 16 KiB head (no kernel reads or writes it), then the
+// accumulator area of the 1..4-row kernel's split column groups (GEMV_ACC_BYTES; zero-filled
+// before a workspace's first call, and every call leaves it zero-filled), then the per-shard
+// partial-sum buffers of all GEMV paths (no required contents).
 constexpr size_t GEMV_COUNTER_BYTES = 16384;
+constexpr size_t GEMV_ACC_BYTES = EXL3_GEMV_ACC_BYTES;
 size_t gemv_workspace_bytes(int rows, int ic, int oc);
 size_t gemv1_slot_bytes(int ic, int oc, int rows);
 bool gemv1_plan_fits(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
                      size_t slot_bytes);
 int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
-                   size_t slot_bytes, hipStream_t stream);
+                   size_t slot_bytes, char* acc, size_t acc_bytes, hipStream_t stream);
 int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows,
                   void* workspace, size_t ws_bytes, hipStream_t stream);
 size_t gemm_workspace_bytes(int rows, int ic, int oc);

@@ -35,15 +35,16 @@ int gemv_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int r
 {
     if (rows < 1 || rows > GV_MAX_ROWS)
         return set_error(EXL3_ERR_ARG, "exl3_gemv: rows=%d is not in 1..%d", rows, GV_MAX_ROWS);
-    size_t need = GEMV_COUNTER_BYTES;
+    size_t need = GEMV_COUNTER_BYTES + GEMV_ACC_BYTES;
     for (int i = 0; i < nshards; i++) need += gemv_workspace_bytes(rows, shards[i].ic, shards[i].oc);
     if (ws_bytes < need)
         return set_error(EXL3_ERR_WORKSPACE, "exl3_gemv: workspace of %zu bytes, %zu needed", ws_bytes, need);
 
-    char* ws = static_cast<char*>(workspace) + GEMV_COUNTER_BYTES;
-    const size_t wsb = need - GEMV_COUNTER_BYTES;
+    char* acc = static_cast<char*>(workspace) + GEMV_COUNTER_BYTES;
+    char* ws = acc + GEMV_ACC_BYTES;
+    const size_t wsb = need - GEMV_COUNTER_BYTES - GEMV_ACC_BYTES;
     if (rows == 1 || (rows <= GV_G1_MAX_ROWS && gemv1_plan_fits(A, shards, nshards, rows, ws, wsb)))
-        return gemv1_dispatch(A, shards, nshards, rows, ws, wsb, stream);
+        return gemv1_dispatch(A, shards, nshards, rows, ws, wsb, acc, GEMV_ACC_BYTES, stream);
     return gemv16_dispatch(A, shards, nshards, rows, ws, wsb, stream);
 }
 

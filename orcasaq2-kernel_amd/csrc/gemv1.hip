@@ -29,12 +29,17 @@
 //      with that workgroup running alone;
 //   3. per segment, the waves' partial sums are added in a fixed order through LDS.  If the
 //      segment lies inside this workgroup's range it is finished here (output Hadamard,
-//      * svh, fp16 store); otherwise the partial goes to this workgroup's slot in the
-//      workspace, and gemv1_finish_kernel, enqueued right after the launch, adds each split
-//      segment's slots in workgroup order (deterministic) and finishes it.  The kernel
-//      boundary orders the slot stores before the reads: no counters, fences or waits
-//      inside the launch (measured on MI355X against a last-arriving-workgroup finish with
-//      agent-scope stores and a counter: 4-9% faster on every 27B projection shape).
+//      * svh, fp16 store).  A segment split over several workgroups is finished in the
+//      same launch without any wait: each workgroup puts its partials through the output
+//      Hadamard and * svh (both linear) and adds them, in fixed point, into the segment's
+//      accumulator words in the workspace with one 64-bit atomic add per output, whose top
+//      bits count the contributions; the add that completes a word's count returns the sum
+//      of all the others, so that lane stores the finished output and clears the word
+//      (g1_acc_add).  One memory round trip, exact integer sums (the same bits whatever
+//      order the workgroups arrive in), no second launch: on MI355X a down_proj call went
+//      from 20.1 to 18.7 us and the 64-layer stack from 5.14 to 4.52 ms per token against
+//      the former finish kernel (which is kept for calls whose accumulators would not fit
+//      the workspace's area: its slots are added in workgroup order after the launch).
 #include "exl3_common.h"
 #include "gemv1_plan.h"
 
@@ -106,6 +111,59 @@ __device__ __forceinline__ void g1_mfma_chunk(const uint32_t (&w)[K + 1], const 
     g1_mfma16<K, CB, 2, 1>(w, a[2], acc, kc);
     g1_mfma16<K, CB, 3, 0>(w, a[3], acc, kc);
     g1_mfma16<K, CB, 3, 1>(w, a[3], acc, kc);
+}
+
+// A transformed partial output as an accumulator increment: one contribution in the count
+// bits plus the value in fixed point, rounded to nearest (the format is gemv1_plan.h's).
+__device__ __forceinline__ unsigned long long g1_fx(float v)
+{
+    v = fminf(fmaxf(v, -G1_FX_MAX), G1_FX_MAX);
+    const long long f = (long long)__builtin_rint((double)v * (double)(1 << G1_FX_FRAC));
+    return (1ull << G1_FX_CBIT) + (unsigned long long)f;
+}
+
+// Split segment S, activation row r, n contributing workgroups, accumulators in a.acc: this
+// workgroup's partial outputs (v0, v1: outputs 2 lane, 2 lane + 1 of the column group) go
+// through the output Hadamard and * svh here -- both linear, so the transformed partials of
+// the n workgroups add up to the finished outputs -- and are added into the segment's words.
+// The add that brings a word's count to n returns the sum of the other n - 1, so its lane
+// holds the finished output: it stores it as fp16 and clears the word for the next call.
+// Integer adds are exact and commute: the result is the same whatever order the workgroups
+// arrive in.  Relaxed agent-scope atomics suffice: every word is read and written only by
+// these adds and the final clear, and the kernel boundary orders the clear before the next
+// call's adds.
+template <bool ONE>
+__device__ __forceinline__ void g1_acc_add(const G1Group& a, const G1Shard* sht, int S, int R, int r, int n,
+                                           float v0, float v1, int lane)
+{
+    const int s = g1_shard_of_seg<ONE>(a, sht, S);
+    const G1Shard& e = g1_sh<ONE>(sht, s);
+    const int cg = S - e.sbeg;
+    wave_fwht128(v0, v1);
+    const uint32_t sv = reinterpret_cast<const uint32_t*>(e.svh + cg * 128)[lane];
+    const unsigned long long m0 = g1_fx(v0 * g1_lo(sv)), m1 = g1_fx(v1 * g1_hi(sv));
+    unsigned long long* p = a.acc + g1_acc_word(S, R, r, lane, 0);
+    const unsigned long long o0 = __hip_atomic_fetch_add(p, m0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long o1 = __hip_atomic_fetch_add(p + 1, m1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // count of an old word: its value part lies in [-2^51, 2^51)
+    constexpr unsigned long long half = 1ull << (G1_FX_CBIT - 1);
+    const unsigned long long last = (unsigned long long)(n - 1);
+    const bool f0 = ((o0 + half) >> G1_FX_CBIT) == last, f1 = ((o1 + half) >> G1_FX_CBIT) == last;
+    if (!f0 && !f1) return;
+    const unsigned long long all = (unsigned long long)n << G1_FX_CBIT;
+    constexpr double unit = 1.0 / (double)(1 << G1_FX_FRAC);
+    const uint16_t h0 = __builtin_bit_cast(uint16_t, (_Float16)(float)((double)(long long)(o0 + m0 - all) * unit));
+    const uint16_t h1 = __builtin_bit_cast(uint16_t, (_Float16)(float)((double)(long long)(o1 + m1 - all) * unit));
+    uint16_t* c = e.C + r * e.ldc + cg * 128 + 2 * lane;
+    if (f0 && f1) {
+        *reinterpret_cast<uint32_t*>(c) = (uint32_t)h0 | ((uint32_t)h1 << 16);
+    } else if (f0) {
+        c[0] = h0;
+    } else {
+        c[1] = h1;
+    }
+    if (f0) __hip_atomic_store(p, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (f1) __hip_atomic_store(p + 1, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ uint32_t g1_dup(float v)
@@ -292,9 +350,11 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
         }
         int g_lo, g_hi;
         g1_contributors<ONE>(a, sht, w.S_first + k, g_lo, g_hi);
-        if (g_hi > g_lo) {
-            // split segment: row r of slot (S, g) holds this workgroup's 128 partials, which
-            // gemv1_finish_kernel adds after the launch
+        if (g_hi > g_lo && a.acc) {
+            g1_acc_add<ONE>(a, sht, w.S_first + k, R, r, g_hi - g_lo + 1, v0, v1, lane);
+        } else if (g_hi > g_lo) {
+            // split segment without accumulators: row r of slot (S, g) holds this workgroup's 128
+            // partials, which gemv1_finish_kernel adds after the launch
             uint64_t* my = reinterpret_cast<uint64_t*>(a.slots + g1_slot(w.S_first + k, g, R)) + lane;
             my[g1_slot_word(0, R, r)] = (uint64_t)__builtin_bit_cast(uint32_t, v0) |
                                         ((uint64_t)__builtin_bit_cast(uint32_t, v1) << 32);
@@ -351,7 +411,7 @@ template <int R, bool ONE>
 __device__ __forceinline__ void g1_finish_body(const G1Group& a, const G1Shard* sht, int S)
 {
     auto sh = [&](int s) -> const G1Shard& { return g1_sh<ONE>(sht, s); };
-    if (S >= a.nsegs) return;
+    if (S >= a.nsegs || a.acc) return;   // a group with accumulators finished in its launch
     const int s = g1_shard_of_seg<ONE>(a, sht, S);
     const int cg = S - sh(s).sbeg;
     int g_lo, g_hi;
@@ -447,7 +507,7 @@ static int g1_launch(const void* fn, void* arg, int G, size_t lds, hipStream_t s
 bool gemv1_plan_fits(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
                      size_t slot_bytes)
 {
-    const int rc = g1_plan(A, shards, nshards, rows, slots, slot_bytes, device_cus(),
+    const int rc = g1_plan(A, shards, nshards, rows, slots, slot_bytes, nullptr, 0, device_cus(),
                            [](const G1Launch&) { return EXL3_OK; });
     if (rc != EXL3_OK) clear_error();
     return rc == EXL3_OK;
@@ -456,9 +516,9 @@ bool gemv1_plan_fits(const uint16_t* A, const GemvShard* shards, int nshards, in
 // The launches of g1_plan: the decode kernel, then (if some segment is split) the finish
 // kernel, one block per segment.
 int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots,
-                   size_t slot_bytes, hipStream_t stream)
+                   size_t slot_bytes, char* acc, size_t acc_bytes, hipStream_t stream)
 {
-    return g1_plan(A, shards, nshards, rows, slots, slot_bytes, device_cus(), [&](const G1Launch& L) {
+    return g1_plan(A, shards, nshards, rows, slots, slot_bytes, acc, acc_bytes, device_cus(), [&](const G1Launch& L) {
         const char* what = "exl3_gemv (1-4 rows, split segments)";
         if (!L.multi) {
             G1Args args = *L.args;

@@ -68,7 +68,8 @@ G1_HD int g1_div(int x, G1Div d)
 struct G1Group {
     const uint16_t* x;         // (nrows, ic) fp16
     int nrows;                 // activation rows, 1 .. R of the kernel
-    float* slots;              // (G + segments) x R x 128 fp32 partials of split segments
+    float* slots;              // (G + segments) x R x 128 fp32 partials of split segments (acc null)
+    unsigned long long* acc;   // segments x R x 128 accumulator words of split segments, or null
     int U, G, ntr, nshards, nsegs;
     int q, r;                  // U = q G + r: workgroup g owns q + (g < r) units
     G1Div dntr, dq, dq1;       // division by ntr, q, q + 1
@@ -477,6 +478,26 @@ G1_HD long g1_slot_word(int t, int R, int r)
     return ((long)t * R + r) * 64;
 }
 
+// Accumulators of split segments.  Each output of a split segment has one 64-bit word: bits
+// 52..63 count the workgroups that have added into it, bits 0..51 hold the sum of their
+// transformed partial outputs as a two's complement fixed-point number with G1_FX_FRAC
+// fractional bits.  A partial is clamped to +-G1_FX_MAX first, so the sum of at most G1_GMAX
+// (2^11) of them stays inside +-2^51 (65504 * 2^24 * 2^11 < 2^51) and never carries into the
+// count.  Outputs of magnitude 2^-14 and above (fp16 normals) keep at least the resolution of
+// their own fp16 spacing; larger partials saturate, and a NaN partial reads as -G1_FX_MAX.
+constexpr int G1_FX_CBIT = 52;
+constexpr int G1_FX_FRAC = 24;
+constexpr float G1_FX_MAX = 65504.f;
+
+// Word of output 2 lane + j (j = 0, 1) of row r of segment S.
+G1_HD long g1_acc_word(int S, int R, int r, int lane, int j)
+{
+    return ((long)S * R + r) * 128 + 2 * lane + j;
+}
+
+// Bytes of a group's accumulators.
+inline size_t g1_acc_bytes(int nsegs, int R) { return (size_t)nsegs * R * 128 * sizeof(unsigned long long); }
+
 // ---------------------------------------------------------------- host: planning
 
 inline G1Div g1_magic(uint32_t d)
@@ -541,9 +562,17 @@ inline long g1_group(G1Group& grp, G1Shard* tab, const GemvShard* shards, const 
     return U;
 }
 
-// Workgroup split of a group of U units into G ranges, and its share of the slots.
-inline int g1_place(G1Group& grp, long U, int G, int R, char* slots, size_t& sbase, size_t slot_bytes)
+// Workgroup split of a group of U units into G ranges, and its share of the slots -- or, when
+// the accumulator area (acc, acc_bytes; abase bytes of it taken by earlier groups of the call)
+// still holds the group's words, its share of that instead.
+inline int g1_place(G1Group& grp, long U, int G, int R, char* slots, size_t& sbase, size_t slot_bytes, char* acc,
+                    size_t acc_bytes, size_t& abase)
 {
+    grp.acc = nullptr;
+    if (acc && abase + g1_acc_bytes(grp.nsegs, R) <= acc_bytes) {
+        grp.acc = reinterpret_cast<unsigned long long*>(acc + abase);
+        abase += g1_acc_bytes(grp.nsegs, R);
+    }
     if (U > (1L << 30))
         return set_error(EXL3_ERR_ARG, "exl3_gemv: %ld tile-row units in one launch (limit 2^30)", U);
     const size_t need = (size_t)(G + grp.nsegs) * R * 128 * sizeof(float);
@@ -563,10 +592,12 @@ inline int g1_place(G1Group& grp, long U, int G, int R, char* slots, size_t& sba
     return EXL3_OK;
 }
 
-// Whether some segment of the group lies in more than one workgroup range (then the
-// launch needs gemv1_finish_kernel): segment S is units S ntr .. S ntr + ntr - 1.
+// Whether some segment of the group lies in more than one workgroup range and the group has
+// no accumulators (then the launch needs gemv1_finish_kernel): segment S is units S ntr ..
+// S ntr + ntr - 1.
 inline bool g1_any_split(const G1Group& grp)
 {
+    if (grp.acc) return false;
     const long big = (long)grp.r * (grp.q + 1);
     auto wg_of = [&](long u) { return u < big ? u / (grp.q + 1) : grp.r + (u - big) / grp.q; };
     for (int S = 0; S < grp.nsegs; S++)
@@ -624,7 +655,7 @@ struct G1Launch {
 // status other than EXL3_OK.
 template <class Emit>
 int g1_plan(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* slots, size_t slot_bytes,
-            int cus, Emit&& emit)
+            char* acc, size_t acc_bytes, int cus, Emit&& emit)
 {
     if (rows < 1 || rows > G1_ROWS) return set_error(EXL3_ERR_ARG, "exl3_gemv: rows=%d is not in 1..%d", rows, G1_ROWS);
     const int R = g1_R(rows);
@@ -647,7 +678,7 @@ int g1_plan(const uint16_t* A, const GemvShard* shards, int nshards, int rows, c
         gidx[j][gn[j]++] = i;
     }
 
-    size_t sbase = 0;
+    size_t sbase = 0, abase = 0;
     bool done[MAXG] = {false};
     for (int j0 = 0; j0 < ng; j0++) {
         if (done[j0]) continue;
@@ -681,7 +712,7 @@ int g1_plan(const uint16_t* A, const GemvShard* shards, int nshards, int rows, c
             G1Args args = {};
             args.grp = m.grp[0];
             for (int i = 0; i < gn[sel[0]]; i++) args.sh[i] = m.sh[i];
-            int rc = g1_place(args.grp, U[0], G[0], R, slots, sbase, slot_bytes);
+            int rc = g1_place(args.grp, U[0], G[0], R, slots, sbase, slot_bytes, acc, acc_bytes, abase);
             if (rc != EXL3_OK) return rc;
             L.one = gn[sel[0]] == 1;
             L.K = gK[sel[0]];
@@ -695,7 +726,7 @@ int g1_plan(const uint16_t* A, const GemvShard* shards, int nshards, int rows, c
         }
         int gb = 0, nb = 0;
         for (int t = 0; t < ns; t++) {
-            const int rc = g1_place(m.grp[t], U[t], G[t], R, slots, sbase, slot_bytes);
+            const int rc = g1_place(m.grp[t], U[t], G[t], R, slots, sbase, slot_bytes, acc, acc_bytes, abase);
             if (rc != EXL3_OK) return rc;
             m.gbeg[t] = gb;
             gb += G[t];

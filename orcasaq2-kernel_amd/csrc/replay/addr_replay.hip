@@ -54,7 +54,7 @@ thread_local std::string g_msg;
 // Fake device buffers: buffer b starts at b << 40, so any address maps back to (buffer,
 // byte offset) and an index outside a buffer cannot land in another one.
 constexpr int FAKE_SHIFT = 40;
-enum Buf { B_NONE, B_X, B_C, B_SLOTS, B_WS, B_TRELLIS = 16, B_SUH = 48, B_SVH = 80, B_AH = 112 };
+enum Buf { B_NONE, B_X, B_C, B_SLOTS, B_WS, B_ACC, B_TRELLIS = 16, B_SUH = 48, B_SVH = 80, B_AH = 112 };
 
 inline uintptr_t fake(int b) { return (uintptr_t)b << FAKE_SHIFT; }
 template <class T>
@@ -102,6 +102,10 @@ struct G1World {
     std::vector<long> unit_base;
     // slots: float offset of each row start -> (S, g, r) that wrote it
     std::map<long, std::tuple<int, int, int>> slot_rows;
+    // accumulator words: byte offset -> (launch * 1e6 + segment, row, output) it sums, and the
+    // adds it has had (each a distinct workgroup)
+    std::map<long, std::tuple<long, int, int>> acc_owner;
+    std::map<long, std::vector<int>> acc_adds;
     long loads = 0, lds_reads = 0;
 };
 
@@ -298,7 +302,41 @@ void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G
             const G1Shard& e = g1_sh<ONE>(sht, s);
             const int cg = S - e.sbeg;
             if (cg < 0 || cg >= e.ncg) fail("segment %d: column group %d of %d", S, cg, e.ncg);
-            if (g_hi > g_lo) {
+            if (g_hi > g_lo && a.acc) {
+                // the transformed partials are added into the segment's words; the add that
+                // completes a word's count (n = g_hi - g_lo + 1 workgroups) stores its output
+                const int n = g_hi - g_lo + 1;
+                for (int r = 0; r < nr; r++)
+                    for (int lane = 0; lane < 64; lane++) {
+                        need_in(reinterpret_cast<const uint32_t*>(e.svh + cg * 128) + lane, 4, B_SVH + gi,
+                                (long)W.sh[gi].oc * 2, "svh load (accumulate)");
+                        for (int j = 0; j < 2; j++) {
+                            const unsigned long long* wp = a.acc + g1_acc_word(S, R, r, lane, j);
+                            need_in(wp, 8, B_ACC, (long)GEMV_ACC_BYTES, "accumulator add");
+                            need_in(wp, 8, B_ACC, off_of(a.acc) + (long)g1_acc_bytes(a.nsegs, R),
+                                    "accumulator add (group share)");
+                            if (off_of(wp) < off_of(a.acc)) fail("accumulator add before the group's share");
+                            const auto key = std::make_tuple((long)launch * 1000000 + S, r, 2 * lane + j);
+                            auto ow = W.acc_owner.find(off_of(wp));
+                            if (ow == W.acc_owner.end()) W.acc_owner[off_of(wp)] = key;
+                            else if (ow->second != key) fail("accumulator word of segment %d row %d output %d shared", S, r, 2 * lane + j);
+                            auto& adds = W.acc_adds[off_of(wp)];
+                            for (int gg : adds)
+                                if (gg == g) fail("wg %d adds twice into segment %d row %d", g, S, r);
+                            adds.push_back(g);
+                            if ((int)adds.size() > n) fail("segment %d row %d: %zu adds, %d workgroups", S, r, adds.size(), n);
+                            if ((int)adds.size() == n) {
+                                const uint16_t* o = e.C + r * e.ldc + cg * 128 + 2 * lane + j;
+                                need_in(o, 2, B_C, (long)W.rows * W.ldc * 2, "output store (last add)");
+                                const long el = off_of(o) / 2;
+                                const long col = el % W.ldc, row = el / W.ldc;
+                                if (row != r || col < W.col0[gi] || col + 1 > W.col0[gi] + W.sh[gi].oc)
+                                    fail("output store at row %ld column %ld outside shard %d", row, col, gi);
+                                W.out[el]++;
+                            }
+                        }
+                    }
+            } else if (g_hi > g_lo) {
                 const float* base = a.slots + g1_slot(S, g, R);
                 for (int r = 0; r < nr; r++) {
                     const uint64_t* row = reinterpret_cast<const uint64_t*>(base) + g1_slot_word(0, R, r);
@@ -403,13 +441,15 @@ void g1_replay_finish(G1World& W, const GemvShard* shards, int R, const G1Group&
 int g1_replay(G1World& W, const GemvShard* shards, int nshards, int cus, long long* stats)
 {
     int launch = 0;
-    const int rc = g1_plan(fake_ptr<uint16_t>(B_X), shards, nshards, W.rows, fake_ptr<char>(B_SLOTS), W.slot_bytes, cus,
+    const int rc = g1_plan(fake_ptr<uint16_t>(B_X), shards, nshards, W.rows, fake_ptr<char>(B_SLOTS), W.slot_bytes,
+                           fake_ptr<char>(B_ACC), GEMV_ACC_BYTES, cus,
                            [&](const G1Launch& L) {
         if (L.lds > 160 * 1024) fail("launch %d: %zu bytes of LDS per workgroup", launch, L.lds);
         if (L.G < 1 || L.G > G1_GMAX * G1_MAXSH) fail("launch %d: %d workgroups", launch, L.G);
         bool any_split = false;
         // split segments by plain division (independent of the magic-number divisions)
         auto note_split = [&](const G1Group& a) {
+            if (a.acc) return;   // split segments finished through the accumulators
             const long big = (long)a.r * (a.q + 1);
             auto wg_of = [&](long u) { return u < big ? u / (a.q + 1) : a.r + (u - big) / a.q; };
             for (int S = 0; S < a.nsegs; S++)
@@ -449,6 +489,8 @@ int g1_replay(G1World& W, const GemvShard* shards, int nshards, int cus, long lo
     if (rc != EXL3_OK) fail("plan refused: %s", g_err);
     for (size_t u = 0; u < W.unit_seen.size(); u++)
         if (W.unit_seen[u] != 1) fail("unit %zu decoded %d times", u, W.unit_seen[u]);
+    // an accumulator word that never reached its count would leave its output unwritten: the
+    // output check below catches it (and so a word not cleared for the next call)
     for (int r = 0; r < W.rows; r++)
         for (size_t gi = 0; gi < W.sh.size(); gi++)
             for (int c = 0; c < W.sh[gi].oc; c++) {

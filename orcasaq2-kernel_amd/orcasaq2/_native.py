@@ -16,7 +16,7 @@ import torch
 
 LIB_NAME = "libexl3hip.so"
 LIB_PATH = os.environ.get("ORCASAQ2_LIB", os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME))
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 CB_3INST, CB_MCG, CB_MUL1 = 0, 1, 2
 GEMV_MAX_ROWS = 16
@@ -167,8 +167,9 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
 
 
-# GEMV workspaces.  A workspace has no required contents; one buffer serves every call
-# issued in order on one stream.
+# GEMV workspaces.  A workspace's accumulator area must be zero before its first call and
+# every call leaves it zero (include/exl3hip.h), so workspaces are made zero-filled and one
+# buffer serves every call issued in order on one stream.
 #   _gemv_ws[(device, stream)]            made by an eager call.
 #   _gemv_ws_cap[(device, stream)]        (capture id, workspace) made inside a graph capture
 #                                         because the stream had no large-enough eager
@@ -177,8 +178,10 @@ def workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 #                                         entry serves that capture only and is simply replaced
 #                                         by the next capture on the stream (the memory may
 #                                         then go to tensors of later captures into the same
-#                                         pool, which torch replays one graph at a time; a
-#                                         workspace's contents matter within one call only).
+#                                         pool, which torch replays one graph at a time: the
+#                                         zero-fill made during the capture is a node of that
+#                                         graph, so each replay clears the area again before
+#                                         its calls).
 # An eager workspace that a captured graph uses is never freed (_gemv_ws_kept): the graph's
 # replays keep writing to it after the eager side has moved on to a larger buffer, and an
 # eager free would hand it to unrelated tensors.  That list grows only when a captured
@@ -198,7 +201,7 @@ def capture_id(device: torch.device) -> int:
 
 
 def _new_gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    return torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+    return torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
 
 
 def gemv_workspace(device: torch.device, nbytes: int) -> torch.Tensor:

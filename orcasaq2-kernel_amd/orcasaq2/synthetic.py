@@ -65,3 +65,46 @@ def stack_shapes() -> dict[str, tuple[int, int]]:
 
 def packed_bytes(ic: int, oc: int, K: int) -> int:
     return ic * oc * K // 8
+
+
+# ---------------------------------------------------------------- device-side generation
+
+CODEBOOK_RMS = 1.2437   # RMS of the 3INST codebook's 2^16 values
+
+
+def linear_gpu(ic: int, oc: int, K: int, gen: torch.Generator, dev: torch.device) -> dict:
+    """One synthetic EXL3 tensor set made on the GPU with a device generator (the same
+    distributions as linear(): uniform 16-bit trellis words, +-1 suh, +-|N(0,1)|/sqrt(ic)
+    svh) -- for the benchmark's many large tensors, which CPU generation would make slow."""
+    t = torch.randint(-32768, 32768, (ic // 16, oc // 16, 16 * K), generator=gen, device=dev,
+                      dtype=torch.int32).to(torch.int16)
+    suh = (torch.randint(0, 2, (ic,), generator=gen, device=dev) * 2 - 1).half()
+    sv = ((torch.randn(oc, generator=gen, device=dev).abs() / math.sqrt(ic)).half()
+          * (torch.randint(0, 2, (oc,), generator=gen, device=dev) * 2 - 1).half())
+    return dict(trellis=t, suh=suh, svh=sv, ic=ic, oc=oc, K=K, codebook=0)
+
+
+def stack_gpu(dev: torch.device, seed: int = 4) -> dict:
+    """Config 4 on the GPU: the 64-layer Qwen-27B-shaped linear stack (K per projection from
+    stack_bits()), the K=6 lm_head, and the int8 embedding table with its fp16 row scales.
+    The svh scales are divided by the codebook RMS, so each projection keeps its input's RMS
+    and 257 chained projections stay finite in fp16.  Returns dict(layers, head, table,
+    scales, nbytes) with nbytes = packed trellis bytes of a token plus one embedding row."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    shapes = stack_shapes()
+
+    def lin(ic, oc, K):
+        d = linear_gpu(ic, oc, K, g, dev)
+        d["svh"] = (d["svh"].float() / CODEBOOK_RMS).half()
+        return d
+
+    layers, nbytes = [], 0
+    for bits in stack_bits():
+        layers.append({n: lin(*shapes[n], bits[n]) for n in shapes})
+        nbytes += sum(packed_bytes(*shapes[n], bits[n]) for n in shapes)
+    head = lin(HIDDEN, VOCAB, 6)
+    nbytes += packed_bytes(HIDDEN, VOCAB, 6)
+    table = torch.randint(-128, 128, (VOCAB, HIDDEN), generator=g, device=dev, dtype=torch.int8)
+    scales = (torch.rand(VOCAB, 1, generator=g, device=dev) * 0.02 + 0.001).half()
+    nbytes += HIDDEN + 2
+    return dict(layers=layers, head=head, table=table, scales=scales, nbytes=nbytes)

@@ -6,7 +6,10 @@ workgroup, so one column group can be split over several workgroups and one work
 touch several column groups (and shards).  These cases cover: a column group inside one
 workgroup, split over several, workgroups spanning 2-3 column groups and a shard
 boundary, waves left without units, every K and both codebooks, grouped shards with mixed
-K, the workspace's reserved head left untouched, determinism, and the config-4
+K, the workspace's reserved head left untouched and its accumulator area left zero after
+calls of every kind (split column groups are summed there and finished by the workgroup whose
+add completes the count), one column group split over some 500 workgroups, determinism, and
+the config-4
 lm_head shape (5120 -> 151936, K = 6) checked on sampled column groups, at 1 row and at
 2..4 rows (the four-row template on more workgroups than stay resident); and a shard too
 large for the four-row template's LDS, which 2..4-row calls hand to gemv16.  Bar: per-row
@@ -93,8 +96,7 @@ def test_gemv1_table_tasks_cross_several_shards(native, oracle, rows):
 
 def test_gemv1_workspace_head_untouched_and_deterministic(native):
     """Repeated calls give identical outputs, and no kernel writes the workspace's reserved
-    16 KiB head (the workspace has no required contents: it comes from torch.empty, so the
-    head is filled with a marker here and must keep it)."""
+    16 KiB head (filled with a marker here, which it must keep)."""
     lin = to_gpu(syn.linear(4096, 2048, 4, seed=77))
     x = syn.activations(1, 4096, torch.Generator().manual_seed(7)).to(dev())
     y0 = native.gemv(x, lin["trellis"], lin["suh"], lin["svh"], 4, 0)
@@ -107,6 +109,59 @@ def test_gemv1_workspace_head_untouched_and_deterministic(native):
     for y in ys:
         assert torch.equal(y, y0)
     assert bool((ws[:16384] == 0xA5).all())
+
+
+ACC0, ACC1 = 16384, 16384 + (2 << 20)   # the workspace's accumulator area
+
+
+@pytest.mark.parametrize("rows", [1, 3])
+def test_gemv1_accumulators_left_zero_between_calls(native, oracle, rows):
+    """Split column groups are summed in the workspace's accumulator words; the add that
+    completes a word's count finishes the output and clears the word.  Calls of different
+    shapes, row counts and shard groupings, interleaved on one workspace, each reproduce
+    their first result bit for bit and leave the whole area zero -- so no call sees another's
+    leftovers."""
+    down = syn.linear(17408, 5120, 4, seed=81)
+    qkv = [syn.linear(5120, oc, K, seed=82 + i) for i, (oc, K) in enumerate([(6144, 4), (1024, 5), (1024, 5)])]
+    xd = syn.activations(rows, 17408, torch.Generator().manual_seed(83))
+    xq = syn.activations(rows, 5120, torch.Generator().manual_seed(84))
+    dg = to_gpu(down)
+    qg = [dict(to_gpu(l), codebook=0) for l in qkv]
+    key = (0, torch.cuda.current_stream(dev()).cuda_stream)
+    first = {}
+    for it in range(3):
+        for name in ("down", "qkv", "down1"):
+            if name == "qkv":
+                y = native.gemv_grouped(xq.to(dev()), qg)
+            else:
+                x = xd.to(dev()) if name == "down" else xd[:1].to(dev())
+                y = native.gemv(x, dg["trellis"], dg["suh"], dg["svh"], 4, 0)
+            torch.cuda.synchronize()
+            ws = native._gemv_ws[key]
+            nz = int((ws[ACC0:ACC1] != 0).sum())
+            assert nz == 0, f"{name} rows={rows} call {it}: {nz} accumulator bytes left non-zero"
+            if it == 0:
+                first[name] = y.clone()
+            else:
+                assert torch.equal(y, first[name]), (name, it)
+    check(first["down"], xd, down, 0, oracle)
+    check(first["down1"], xd[:1], down, 0, oracle)
+    col = 0
+    for l in qkv:
+        check(first["qkv"][:, col:col + l["oc"]], xq, l, 0, oracle)
+        col += l["oc"]
+
+
+def test_gemv1_one_column_group_over_many_workgroups(native, oracle):
+    """A 262144 -> 128 shard (K = 2): its single column group's 16384 tile rows are split over
+    every workgroup of the launch (some 500), all adding into the same 128 words."""
+    lin = syn.linear(262144, 128, 2, seed=85)
+    x = syn.activations(1, 262144, torch.Generator().manual_seed(86))
+    g = to_gpu(lin)
+    ys = [native.gemv(x.to(dev()), g["trellis"], g["suh"], g["svh"], 2, 0) for _ in range(3)]
+    torch.cuda.synchronize()
+    check(ys[0], x, lin, 0, oracle)
+    assert torch.equal(ys[1], ys[0]) and torch.equal(ys[2], ys[0])
 
 
 def test_gemv1_lm_head_sampled_column_groups(native, oracle):
