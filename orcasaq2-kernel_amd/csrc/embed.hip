@@ -77,7 +77,10 @@ int embed_dispatch(const int8_t* table, const void* scales, int scale_dtype, con
                    void* out, long n_ids, int vocab, int dim, hipStream_t stream)
 {
     if (n_ids == 0) return EXL3_OK;
-    if (n_ids > 0x7fffffffL) return set_error(EXL3_ERR_ARG, "exl3_embed_int8_gather: %ld ids (at most 2^31 - 1)", n_ids);
+    // one workgroup per id, and a launch holds at most 2^32 - 1 work-items
+    const long max_ids = 0xffffffffL / EMB_THREADS;
+    if (n_ids > max_ids)
+        return set_error(EXL3_ERR_ARG, "exl3_embed_int8_gather: %ld ids (at most %ld)", n_ids, max_ids);
     hipLaunchKernelGGL(embed_int8_kernel, dim3((unsigned)n_ids), dim3(EMB_THREADS), 0, stream, table, scales,
                        scale_dtype, ids, out, vocab, dim);
     return check_launch("exl3_embed_int8_gather");

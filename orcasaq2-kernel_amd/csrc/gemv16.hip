@@ -293,6 +293,16 @@ static const void* g16_fn_kcb(int K, int cb, bool one)
 
 size_t gemv16_shard_bytes(int ic, int oc) { return g16_shard_bytes(ic, oc); }
 
+// A decode launch's dynamic LDS above 64 KiB needs the kernel's opt-in first (the plan allows
+// up to a CU's 160 KiB when a launch's ranges are long).
+static void g16_lds_optin(const void* fn, size_t lds)
+{
+    if (lds > 64 * 1024) {
+        hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        (void)hipGetLastError();
+    }
+}
+
 int gemv16_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws, size_t ws_bytes,
                     hipStream_t stream)
 {
@@ -312,6 +322,7 @@ int gemv16_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int
             const void* fn = g16_fn_kcb(L.K, L.cb, L.one);
             if (!fn) return set_error(EXL3_ERR_ARG, "%s: K=%d is not in 1..8", what, L.K);
             void* kargs[] = {&args};
+            g16_lds_optin(fn, L.lds);
             hipLaunchKernel(fn, dim3(L.G), dim3(64 * G1_NW), kargs, L.lds, stream);
             int rc = check_launch(what);
             if (rc != EXL3_OK) return rc;
@@ -324,6 +335,7 @@ int gemv16_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int
         const void* fn = L.cb == CB_MCG ? reinterpret_cast<const void*>(&gemv16_multi_kernel<CB_MCG>)
                                         : reinterpret_cast<const void*>(&gemv16_multi_kernel<CB_3INST>);
         void* kargs[] = {&m};
+        g16_lds_optin(fn, L.lds);
         hipLaunchKernel(fn, dim3(L.G), dim3(64 * G1_NW), kargs, L.lds, stream);
         int rc = check_launch(what);
         if (rc != EXL3_OK) return rc;

@@ -8,10 +8,11 @@ kernels only enqueue on the current stream, so it can be captured in a HIP graph
 Dispatch on the number of activation rows (reference: orcasaq2/ops.py:25, 46-59):
   * rows <= 16            fused decode-GEMV (exl3_gemv): packed words streamed from HBM and
                           decoded in registers, never stored; rows 1..4: one persistent kernel
-                          (MFMA multiply-accumulate, split column groups finished by a second
-                          kernel; rows 2..4 of very wide shards take MFMA partial sums + a
-                          reduce kernel); rows 5..16: the same decode on 4 x 2-tile units, one
-                          MFMA serving all rows; output Hadamard and svh at the end;
+                          (MFMA multiply-accumulate; a column group split over workgroups is
+                          summed in fixed point in the workspace and finished by the workgroup
+                          whose add completes it); rows 5..16, and 2..4-row shards too large for
+                          that kernel's tables: the same decode on 4 x 2-tile units, one MFMA
+                          serving all rows; output Hadamard and svh at the end;
   * 16 < rows <= GEMM_MAX_ROWS
                           fused decode-GEMM (exl3_gemm): Hadamard pass over x, then stream-K
                           tiles decoded straight into MFMA operands, output Hadamard in the

@@ -86,6 +86,9 @@ def test_other_entry_points_reject_bad_arguments(native):
     assert L.exl3_embed_int8_gather(fake, fake, 0, fake, fake, 4, 100, 10, None) == 1  # dim % 4
     assert L.exl3_embed_int8_gather(fake, fake, 5, fake, fake, 4, 100, 16, None) == 1  # dtype
     assert L.exl3_embed_int8_gather(None, None, 0, None, None, 0, 0, 16, None) == 0    # empty: no-op
+    # one 256-lane workgroup per id: more than (2^32 - 1) / 256 ids would exceed a launch
+    assert L.exl3_embed_int8_gather(fake, fake, 0, fake, fake, 1 << 24, 100, 16, None) == 1
+    assert "at most 16777215" in _err(native)
     sh = (native.Shard * 2)()
     sh[0] = native.Shard(0x10000, 0x10000, 0x10000, 0x10000, 512, 256, 4, 0)
     sh[1] = native.Shard(0x10000, 0x10000, 0x10000, 0x10100, 512, 256, 5, 0)

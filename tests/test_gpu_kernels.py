@@ -140,8 +140,8 @@ def check_linear_out(y, x, lin, cb, oracle, W=None):
 @pytest.mark.parametrize("K", range(1, 9))
 @pytest.mark.parametrize("rows", [1, 4, 5, 16])
 def test_gemv_small_all_K(native, oracle, K, rows):
-    """1..4 rows: the persistent kernel (4 rows in the MFMA's A operand); 5..16: 16-row
-    stream-K tiles"""
+    """1..4 rows: the persistent kernel (4 rows in the MFMA's A operand); 5..16: gemv16 (the
+    batch-1 decode on 4 x 2-tile units, one MFMA serving all 16 rows)"""
     lin = syn.linear(512, 384, K, seed=100 + K)
     x = syn.activations(rows, 512, torch.Generator().manual_seed(rows))
     d = to_gpu(lin)

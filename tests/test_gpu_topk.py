@@ -2,8 +2,8 @@
 oracle's restatement (oracle.topk_rows: largest first, equal values by smaller column, NaN
 above every number, -0 == +0), bit-exact in values and columns.
 
-Shapes: the K=6 lm_head's vocabulary (151936) at 1, 3 and 16 rows; one stage-1 chunk
-exactly (16384), one column past it, a last chunk holding fewer than k columns; tiny rows
+Shapes: the K=6 lm_head's vocabulary (151936) at 1, 3 and 16 rows; four stage-1 chunks of
+4096 exactly (16384), one column past them, a last chunk holding fewer than k columns; tiny rows
 (n = k, n = 1); the 2^19-column bound; a strided view read in place (ld > n) and rows the
 wrapper first copies (n % 8 != 0).  Values: normal logits (many fp16 ties at this size),
 rows drawn from a handful of values (ties everywhere, also across chunk boundaries), all-equal

@@ -221,6 +221,71 @@ def test_register_and_patch_embedding_constructors(native):
     assert plain.quant_method is None
 
 
+_PLUGIN_PROCESS = r"""
+import importlib, json, sys, tomllib
+sys.path.insert(0, "orcasaq2-kernel_amd")
+role = sys.argv[1]
+# the entry point vLLM resolves in every process it starts (pyproject.toml, vllm.general_plugins)
+spec = tomllib.load(open("pyproject.toml", "rb"))["project"]["entry-points"]["vllm.general_plugins"]["orcasaq2"]
+mod, fn = spec.split(":")
+register = getattr(importlib.import_module(mod), fn)
+register()
+register()                                   # vLLM may load general plugins more than once
+import orcasaq2
+from orcasaq2 import _vllm_compat as vc
+from orcasaq2.config import Exl3Config, Exl3LinearMethod
+from orcasaq2.heads import Exl3EmbeddingMethod
+out = {"role": role, "registered": vc.quant_registry()["exl3"] is Exl3Config,
+       "patched": bool(vc.VocabParallelEmbedding.__dict__.get("_orca_patched"))
+                  and bool(vc.ParallelLMHead.__dict__.get("_orca_patched"))}
+cfg = Exl3Config.from_config({"head_bits": 6})
+class Cfg:
+    quant_config = cfg
+with vc.set_current_vllm_config(Cfg()):
+    lin = vc.LinearBase(256, 384, quant_config=cfg, prefix="model.layers.0.self_attn.qkv_proj",
+                        output_partition_sizes=[128, 128, 128])
+    emb = vc.VocabParallelEmbedding(64, 8)
+    head = vc.ParallelLMHead(64, 8, prefix="lm_head")
+out["linear"] = type(lin.quant_method).__name__
+out["placeholders"] = sorted(n for n, _ in lin.named_parameters())
+out["embedding"] = isinstance(emb.quant_method, Exl3EmbeddingMethod)
+out["lm_head"] = isinstance(head.quant_method, Exl3LinearMethod)
+print(json.dumps(out))
+"""
+
+
+def test_plugin_in_fresh_processes_like_vllms_server_engine_and_worker():
+    """vLLM loads general plugins in each process it starts (API server, engine core, each
+    worker), each a fresh interpreter (reference orcasaq2/__init__.py:64-94).  Three fresh
+    processes run at once, each resolving the pyproject entry point, calling register() twice
+    and building stand-in layers: every one must import cleanly, register "exl3" once, wrap
+    the embedding and lm_head constructors, and give a fused linear its six placeholders."""
+    import json
+    import os
+    import subprocess
+    import sys
+    if sys.version_info < (3, 11):
+        pytest.importorskip("tomli")
+        code = _PLUGIN_PROCESS.replace("import importlib, json, sys, tomllib", "import importlib, json, sys\nimport tomli as tomllib")
+    else:
+        code = _PLUGIN_PROCESS
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    procs = [subprocess.Popen([sys.executable, "-c", code, role], cwd=root, stdout=subprocess.PIPE,
+                              stderr=subprocess.PIPE, text=True)
+             for role in ("api_server", "engine_core", "worker_0")]
+    outs = []
+    for p in procs:
+        so, se = p.communicate(timeout=300)
+        assert p.returncode == 0, se
+        outs.append(json.loads(so.strip().splitlines()[-1]))
+    assert [o["role"] for o in outs] == ["api_server", "engine_core", "worker_0"]
+    for o in outs:
+        assert o["registered"] and o["patched"], o
+        assert o["linear"] == "Exl3LinearMethod", o
+        assert o["placeholders"] == ["mcg", "mul1", "suh", "svh", "trellis", "weight"], o
+        assert o["embedding"] and o["lm_head"], o
+
+
 def test_product_op_has_no_cpu_path_without_the_test_kernel():
     import subprocess
     import sys

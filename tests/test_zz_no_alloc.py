@@ -2,10 +2,12 @@
 file-scope device array of the library), called through the C ABI against
 exl3_gemv_grouped with a caller workspace on the same inputs.
 
-The kernels are the same and their split reductions run in a fixed order, so the two
-outputs must agree bit for bit; each call is also checked against the fp64 oracle at the
-GEMV bar (per-row relative L2 error <= 1e-3).  Two calls in a row on one stream, the second
-smaller, cover the reuse of the array (its counters left zero by the first call); a
+The kernels are the same and their split reductions are exact (fixed-point sums at 1..4
+rows) or run in a fixed order (5..16 rows), so the two outputs must agree bit for bit; each
+call is also checked against the fp64 oracle at the GEMV bar (per-row relative L2 error <=
+1e-3).  Two calls in a row on one stream, the second smaller, cover the reuse of the array
+(its accumulator area, zero when the library loads, is left zero by every call) at 1, 4 and
+16 rows; 16 rows on a lm_head-width shard covers the largest scratch the array holds; a
 captured-and-replayed call covers a caller that cannot allocate because it is under graph
 capture.  The size limit is a host check, tested without a GPU call.
 """
@@ -70,7 +72,7 @@ def _check_oracle(oracle, y, x, lins):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("rows", [1, 4])
+@pytest.mark.parametrize("rows", [1, 4, 16])
 def test_static_matches_workspace_twice_second_smaller(native, oracle, rows):
     # first: the 27B qkv (three shards, K = 4, 5, 5); second: one small shard
     for ic, ocs_ks, seed in ((syn.HIDDEN, [(syn.Q_OUT, 4), (syn.KV_OUT, 5), (syn.KV_OUT, 5)], 11),
@@ -81,6 +83,41 @@ def test_static_matches_workspace_twice_second_smaller(native, oracle, rows):
         assert not torch.isnan(y_static).any()
         assert torch.equal(y_static, y_ws)
         _check_oracle(oracle, y_static, x, lins)
+
+
+@pytest.mark.gpu
+def test_static_lm_head_width_at_16_rows(native, oracle):
+    """The K=6 lm_head shape (5120 -> 151936) at 16 rows: the 5..16-row path's fragments and
+    slots for 1187 column groups, the most scratch a 27B call asks of the array.  Static and
+    workspace outputs agree bit for bit; two column groups are checked against the oracle."""
+    dev = torch.device("cuda", 0)
+    L = native.lib()
+    g = torch.Generator(device=dev).manual_seed(31)
+    lin = syn.linear_gpu(syn.HIDDEN, syn.VOCAB, 6, g, dev)
+    x = syn.activations(16, syn.HIDDEN, torch.Generator().manual_seed(31))
+    xd = x.to(dev)
+    stream = P(torch.cuda.current_stream(dev).cuda_stream)
+    print("static gemv: rows=16 lm_head 5120->151936 K=6", flush=True)
+    y_static = torch.full((16, syn.VOCAB), float("nan"), dtype=torch.float16, device=dev)
+    arr = _table(native, [lin], y_static, syn.VOCAB)
+    assert L.exl3_gemv_grouped_workspace_bytes(arr, 1, 16, syn.HIDDEN) <= (20 << 20)
+    rc = L.exl3_gemv_grouped_static(P(xd.data_ptr()), arr, 1, 16, syn.HIDDEN, stream)
+    assert rc == 0, L.exl3_last_error().decode()
+    y_ws = torch.full_like(y_static, float("nan"))
+    arr2 = _table(native, [lin], y_ws, syn.VOCAB)
+    nbytes = L.exl3_gemv_grouped_workspace_bytes(arr2, 1, 16, syn.HIDDEN)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    rc = L.exl3_gemv_grouped(P(xd.data_ptr()), arr2, 1, P(ws.data_ptr()), nbytes, 16, syn.HIDDEN, stream)
+    assert rc == 0, L.exl3_last_error().decode()
+    torch.cuda.synchronize()
+    assert not torch.isnan(y_static).any()
+    assert torch.equal(y_static, y_ws)
+    for cg in (0, 1000):
+        sl = slice(cg * 128, (cg + 1) * 128)
+        t = lin["trellis"][:, cg * 8:(cg + 1) * 8].contiguous().cpu()
+        ref = oracle.shard_gemm_ref(x.numpy(), t, lin["suh"].cpu().numpy(), lin["svh"][sl].cpu().numpy(), 6, 0)
+        err = oracle.rel_err_rows(y_static[:, sl].cpu().numpy(), ref)
+        assert err.max() <= REL_TOL, (cg, err.max())
 
 
 @pytest.mark.gpu
