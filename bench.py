@@ -137,7 +137,8 @@ def gpu_bench(args) -> dict:
 
     g_warm = capture(0, max(args.warmup, 1))
     g_timed = capture(args.warmup, args.steps)
-    g_warm.replay()
+    _settle(g_warm.replay, side)          # clocks out of their idle state (not timed)
+    g_warm.replay()                       # the W warm-up steps
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     g_timed.replay()
@@ -147,7 +148,7 @@ def gpu_bench(args) -> dict:
     per_k = {}
     for K in Ks:
         gk = capture(args.warmup, args.steps, only=(K,))
-        gk.replay()
+        _settle(gk.replay, side)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(side)
@@ -192,13 +193,37 @@ def _graph(dev, fn, settle=True):
     return graph, side
 
 
-def _time_graph(graph, side, reps: int) -> float:
-    """Seconds per replay: one warm replay, then `reps` replays between HIP events recorded
-    on the replay stream."""
+SETTLE_S = 0.25   # seconds of sustained GPU work before any timed region
+
+
+def _settle(replay, side, seconds: float = SETTLE_S) -> None:
+    """Runs replay() (one graph replay, or one eager step) on `side` until `seconds` of GPU time
+    have passed.  The GPU's clocks rise from their idle state only over the first tens of
+    milliseconds of sustained work: measured on MI355X from idle, a down_proj K=5 GEMV call
+    takes 19.6-20.3 us in the first ~3 ms and 16.4-17.0 us from ~20 ms on, the M=2048 prefill
+    GEMM 456-514 us at first and ~400 us from ~35 ms on.  A serving GPU runs busy, so the
+    timed regions start from those steady clocks; the settle is never part of a timing."""
     import torch
-    with torch.cuda.stream(side):
-        graph.replay()
-    torch.cuda.synchronize()
+    spent, n = 0.0, 1
+    while spent < seconds:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(side)
+        with torch.cuda.stream(side):
+            for _ in range(n):
+                replay()
+        e1.record(side)
+        torch.cuda.synchronize()
+        spent += e0.elapsed_time(e1) * 1e-3
+        # small batches: right after one batch of some hundreds of replays, the next replay
+        # measured ~3x its steady time (the runtime's own cost, not the GPU's)
+        n = min(2 * n, 16)
+
+
+def _time_graph(graph, side, reps: int) -> float:
+    """Seconds per replay: replays until the clocks have settled (_settle), then `reps`
+    replays between HIP events recorded on the replay stream."""
+    import torch
+    _settle(graph.replay, side)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(side)
     with torch.cuda.stream(side):
@@ -210,7 +235,7 @@ def _time_graph(graph, side, reps: int) -> float:
 
 
 def prefill_bench(reps: int) -> dict:
-    """Prefill at few rows (17..768), the 27B layer shapes: per shape and row count the fused
+    """Prefill at 17..4096 rows, the 27B layer shapes: per shape and row count the fused
     stream-K GEMM (exl3_gemm) against the op's reconstruct branch (had_r_128, reconstruct
     to (oc, ic), library fp16 transposed-B GEMM, had_r_128); per fused layer (qkv, gate_up)
     the grouped launch (exl3_gemm_grouped) against the per-shard fused GEMMs + cat and the
@@ -236,7 +261,7 @@ def prefill_bench(reps: int) -> dict:
                             ("q 5120->6144 K4", 5120, 6144, 4)):
         d = _rand_linear(ic, oc, K, g, dev)
         row = {}
-        for M in (17, 40, 64, 80, 128, 144, 256, 384, 768):
+        for M in (17, 40, 64, 80, 128, 144, 256, 384, 768, 1024, 2048, 4096):
             x = torch.randn(M, ic, generator=g, device=dev).half()
             y = torch.empty(M, oc, dtype=torch.half, device=dev)
             row[M] = {"fused": t_of(lambda: _native.gemm(x, d["trellis"], d["suh"], d["svh"], K, 0, out=y)),
@@ -428,6 +453,8 @@ def config3_bench(reps: int) -> dict:
     t_rect = _time_graph(grt, side_rt, reps)
     op()
     torch.cuda.synchronize()
+    cur = torch.cuda.current_stream(dev)
+    _settle(op, cur)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -571,7 +598,8 @@ def ceiling_bench(reps: int) -> dict:
     gemv1_kernel but stop short of parts of its work (empty grid / loads only / loads +
     three-instruction decode / loads + decode + the 16 MFMAs per unit with activations from a
     constant LDS table), timed per call in HIP graphs over rotating weight copies exactly like
-    config 1, beside the product GEMV itself; then the issue cost of the decode's instructions
+    config 1, beside a plain coalesced dwordx4 stream of the same bytes (what HBM gives a
+    read of this size at all) and the product GEMV itself; then the issue cost of the decode's instructions
     and of the MFMA forms (8 independent chains per wave, 8 waves per SIMD)."""
     import ctypes
     import torch
@@ -583,6 +611,7 @@ def ceiling_bench(reps: int) -> dict:
     M.exl3m_stream.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                ctypes.c_void_p, ctypes.c_void_p]
     M.exl3m_ops.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    M.exl3m_plain.argtypes = [ctypes.c_void_p, ctypes.c_long, ctypes.c_void_p, ctypes.c_void_p]
     M.exl3m_sink_bytes.restype = ctypes.c_long
     M.exl3m_stream_workgroups.argtypes = [ctypes.c_int, ctypes.c_int]
     M.exl3m_sink_bytes.argtypes = [ctypes.c_int, ctypes.c_int]
@@ -609,6 +638,16 @@ def ceiling_bench(reps: int) -> dict:
             gr, side = _graph(dev, run, settle=False)
             us = _time_graph(gr, side, reps) / calls * 1e6
             row[names[mode]] = {"us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1)}
+
+        def plain():
+            st = torch.cuda.current_stream(dev).cuda_stream
+            for i in range(calls):
+                rc = M.exl3m_plain(copies[i % len(copies)]["trellis"].data_ptr(), nbytes, sink.data_ptr(), st)
+                if rc != 0:
+                    raise RuntimeError(f"exl3m_plain K={K}: {rc}")
+        gr, side = _graph(dev, plain, settle=False)
+        us = _time_graph(gr, side, reps) / calls * 1e6
+        row["plain dwordx4 stream of the same bytes"] = {"us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1)}
 
         def prod():
             for i in range(calls):

@@ -19,6 +19,10 @@
 //           operand, mfma16_group) instead of 16 v_mfma_f32_4x4x4_16b_f16.
 // Every accumulator reaches a store that is never taken, so no work is optimised away.
 //
+// The plain stream (exl3m_plain) reads the same bytes without the GEMV's layout: 16-byte
+// pieces at a grid stride, four loads in flight per lane, the same grid of 4 workgroups of
+// 8 waves per CU -- what HBM gives a read of this size in its most regular access pattern.
+//
 // The op kernels time chains of one instruction (8 independent chains per wave, 8 waves
 // per SIMD, 4 workgroups of 8 waves per CU) to give the issue cost per wave64 instruction.
 #include "../exl3_common.h"
@@ -261,6 +265,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(8, 8)))
     if (s == 0x9e3779b9u || f == 1234.5f) sink[blockIdx.x * 64 * NW + threadIdx.x] = s;
 }
 
+__global__ __launch_bounds__(64 * NW) void plain_kernel(const uint4* __restrict__ p, long n16, uint32_t* sink)
+{
+    const long tid = (long)blockIdx.x * 64 * NW + threadIdx.x, nt = (long)gridDim.x * 64 * NW;
+    uint32_t x = 0;
+    long i = tid;
+    for (; i + 3 * nt < n16; i += 4 * nt) {
+        const uint4 a = p[i], b = p[i + nt], c = p[i + 2 * nt], d = p[i + 3 * nt];
+        x ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+    }
+    for (; i < n16; i += nt) {
+        const uint4 a = p[i];
+        x ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    if (x == 0x9e3779b9u) sink[tid] = x;
+}
+
 static int cus()
 {
     int dev = 0, n = 0;
@@ -312,6 +332,16 @@ int exl3m_stream(int mode, const void* trellis, int ic, int oc, int K, void* sin
                    : mode == 3 ? stream_fn<3>(K) : stream_fn<4>(K);
     void* args[] = {(void*)&trellis, (void*)&ntr, (void*)&oc16, (void*)&U, (void*)&sink};
     hipLaunchKernel(fn, dim3(G), dim3(64 * NW), args, 0, static_cast<hipStream_t>(stream));
+    return (int)hipGetLastError();
+}
+
+// The plain stream over nbytes (a multiple of 16, 16-byte aligned) at trellis; 4 workgroups per CU.
+int exl3m_plain(const void* trellis, long nbytes, void* sink, void* stream)
+{
+    if (nbytes <= 0 || nbytes % 16 || ((uintptr_t)trellis & 15)) return -1;
+    const long n16 = nbytes / 16;
+    hipLaunchKernelGGL(plain_kernel, dim3(4 * cus()), dim3(64 * NW), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint4*>(trellis), n16, static_cast<uint32_t*>(sink));
     return (int)hipGetLastError();
 }
 

@@ -21,7 +21,9 @@ Dispatch on the number of activation rows (reference: orcasaq2/ops.py:25, 46-59)
                           reconstruct branch measured faster (_fused_gemm_faster);
   * rows > GEMM_MAX_ROWS  the reference's reconstruct branch: had_r_128(x, suh), dense W_q
                           (decoded transposed, (oc, ic)) into a scratch freed on exit, library
-                          fp16 transposed-B GEMM, had_r_128(y, svh).
+                          fp16 transposed-B GEMM, had_r_128(y, svh) -- except shards of 8192+
+                          inputs up to WIDE_FUSED_MAX_ROWS rows (fused, measured faster) while
+                          the row knob is at its default.
 The op is registered for the "cuda" device type (ROCm) only: there is no CPU path.
 """
 
@@ -33,8 +35,13 @@ from torch import Tensor
 from . import _native
 
 # Rows at or below which the fused kernels are used (the reference's default and env knob,
-# orcasaq2/ops.py:22-25).  Above it the dense W_q is rebuilt once and a library GEMM runs.
+# orcasaq2/ops.py:22-25).  Above it the dense W_q is rebuilt once and a library GEMM runs --
+# except, while the knob is left at its default, for shards of 8192 or more inputs (down_proj)
+# up to WIDE_FUSED_MAX_ROWS rows, where the fused kernel measured faster (_fused_gemm_faster).
+# Setting the knob makes it the hard switch of the reference.
 GEMM_MAX_ROWS = int(os.environ.get("ORCA_EXL3_GEMM_MAX_ROWS", "144"))
+GEMM_MAX_ROWS_SET = "ORCA_EXL3_GEMM_MAX_ROWS" in os.environ
+WIDE_FUSED_MAX_ROWS = 1024
 GEMV_MAX_ROWS = _native.GEMV_MAX_ROWS
 
 
@@ -48,16 +55,28 @@ def exl3_K(trellis: Tensor):
 
 def _fused_gemm_faster(rows: int, ic: int, oc: int) -> bool:
     """Whether the fused decode-GEMM beats the reconstruct branch for one shard at
-    GEMV_MAX_ROWS < rows <= GEMM_MAX_ROWS.  Measured on MI355X (us per call, HIP graph,
-    fused / reconstruct branch): 17408 -> 5120 wins at every row count to 768 (144 rows:
-    121 / 178); 5120 -> 17408 wins to 128 rows (81 / 87) and loses at 144 (117 / 99);
-    5120 -> 6144 ties at 64 (47 / 46) and loses from 80 (60 / 49) to 144 (71 / 54).  With
-    ic in [4096, 8192) the dense W_q is cheap to rebuild and the library GEMM short, so above
-    64 rows the branch wins unless oc is at least twice ic and rows stay within 128; other
-    input widths (unmeasured below 4096) keep the fused path."""
-    if rows <= 64 or ic >= 8192 or ic < 4096:
+    GEMV_MAX_ROWS < rows <= GEMM_MAX_ROWS, or (ic >= 8192) at up to WIDE_FUSED_MAX_ROWS rows.
+    Measured on MI355X at settled clocks (us per call, HIP graph, fused / reconstruct branch):
+    17408 -> 5120 wins at every row count to 1024 (144 rows: 117 / 176, 256: 117 / 228, 1024:
+    224 / 310) and loses from 2048 (405 / 370); 5120 -> 17408 wins to 128 rows (79 / 85) and
+    loses at 144 (112 / 94); 5120 -> 6144 ties at 64 (47 / 46) and loses from 80 (60 / 49) to
+    144 (69 / 52).  With ic in [4096, 8192) the dense W_q is cheap to rebuild and the library
+    GEMM short, so above 64 rows the branch wins unless oc is at least twice ic and rows stay
+    within 128; other input widths (unmeasured below 4096) keep the fused path to
+    GEMM_MAX_ROWS."""
+    if ic >= 8192:
+        return rows <= WIDE_FUSED_MAX_ROWS
+    if rows <= 64 or ic < 4096:
         return True
     return rows <= 128 and oc >= 2 * ic
+
+
+def _fused_route(rows: int, ic: int, oc: int) -> bool:
+    """The fused decode-GEMM for rows > GEMV_MAX_ROWS: within GEMM_MAX_ROWS where it measured
+    faster, beyond it only for wide inputs while the knob is at its default."""
+    if rows <= GEMM_MAX_ROWS:
+        return _fused_gemm_faster(rows, ic, oc)
+    return not GEMM_MAX_ROWS_SET and ic >= 8192 and _fused_gemm_faster(rows, ic, oc)
 
 
 def _shard_gemm_impl(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, oc: int, k: float,
@@ -70,7 +89,7 @@ def _shard_gemm_impl(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, oc: i
         return x.new_empty((0, oc), dtype=torch.half)
     if rows <= GEMV_MAX_ROWS:
         return _native.gemv(x, trellis, suh, svh, k, cb)
-    if rows <= GEMM_MAX_ROWS and _fused_gemm_faster(rows, ic, oc):
+    if _fused_route(rows, ic, oc):
         return _native.gemm(x, trellis, suh, svh, k, cb)
     # reconstruct branch: dense W_q lives only for the duration of the call, decoded as
     # W_q^T (oc, ic) so the library runs its transposed-B GEMM (measured 15-20% faster than

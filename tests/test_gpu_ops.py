@@ -66,6 +66,27 @@ def test_shard_gemm_routing_by_shape(native, oracle, rows, oc):
     assert oracle.rel_err_rows(y.cpu().numpy(), ref(oracle, x, lin)).max() <= 1e-3
 
 
+@pytest.mark.parametrize("rows", [512, 2048])
+def test_shard_gemm_down_proj_prefill_op_route(native, oracle, rows):
+    """The op on config 3's shape, down_proj 17408 -> 5120 at K=4, at 512 rows (above
+    GEMM_MAX_ROWS: the fused GEMM, which measured faster there for wide inputs) and 2048 rows
+    (the reconstruct branch, faster at that size): whichever route the op takes, sampled rows
+    match the oracle."""
+    lin = syn.linear(17408, 5120, 4, seed=3)
+    x = syn.activations(rows, 17408, torch.Generator().manual_seed(rows + 33))
+    d = on(lin)
+    fused = O._fused_route(rows, 17408, 5120)
+    if not O.GEMM_MAX_ROWS_SET:
+        assert fused == (rows <= O.WIDE_FUSED_MAX_ROWS)
+    print(f"shard_gemm down_proj rows={rows} fused={fused}", flush=True)
+    y = torch.ops.orcasaq2.shard_gemm(x.to(D), d["trellis"], d["suh"], d["svh"], 5120, 4.0, False, False)
+    assert y.shape == (rows, 5120) and y.dtype == torch.half
+    W = oracle.reconstruct_f16(lin["trellis"], 4, 0)
+    idx = torch.tensor([0, 1, 63, 64, rows // 2, rows - 1])
+    want = oracle.shard_gemm_ref(x[idx].numpy(), lin["trellis"], lin["suh"].numpy(), lin["svh"].numpy(), 4, 0, W=W)
+    assert oracle.rel_err_rows(y[idx.to(D)].cpu().numpy(), want).max() <= 1e-3
+
+
 def _two_shard_step(rows, ic=1024):
     lins = [syn.linear(ic, oc, K, seed=i) for i, (oc, K) in enumerate([(512, 4), (256, 5)])]
     ds = [on(l) for l in lins]

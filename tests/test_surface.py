@@ -311,3 +311,9 @@ def test_fused_gemm_routing_follows_the_measured_crossovers():
     assert f(64, 5120, 6144) and not f(80, 5120, 6144) and not f(144, 5120, 6144)   # q / o-like
     assert f(128, 5120, 17408) and not f(144, 5120, 17408)                           # gate / up
     assert f(144, 512, 256) and f(144, 2048, 1024)     # unmeasured narrow inputs keep the fused path
+    # above GEMM_MAX_ROWS: wide inputs (down_proj) stay fused to 1024 rows, the rest reconstruct
+    r = ops._fused_route
+    if not ops.GEMM_MAX_ROWS_SET:
+        assert r(145, 17408, 5120) and r(512, 17408, 5120) and r(1024, 17408, 5120)
+        assert not r(1025, 17408, 5120) and not r(2048, 17408, 5120)
+    assert not r(145, 5120, 17408) and not r(2048, 5120, 6144) and not r(145, 512, 256)
