@@ -48,7 +48,7 @@ extern "C" {
 
 #define EXL3_GEMV_MAX_ROWS 16
 /* Zero-filled accumulator area at byte 16384 of every GEMV workspace (see above). */
-#define EXL3_GEMV_ACC_BYTES (2u << 20)
+#define EXL3_GEMV_ACC_BYTES (6u << 20)
 #define EXL3_MAX_SHARDS 64
 
 /* Message for the last failing call on this thread ("" if none). */
@@ -138,7 +138,7 @@ int exl3_gemv_grouped(const void* A, const exl3_shard_t* shards, int nshards, vo
  * exl3_gemv_grouped without a workspace argument: it allocates nothing (no hipMalloc, no
  * library allocation), for callers that cannot allocate -- code under HIP-graph capture,
  * serving loops that forbid device allocation.  No counterpart in the reference.
- * The scratch is a file-scope device array of EXL3_STATIC_SCRATCH_BYTES (20 MiB), one per
+ * The scratch is a file-scope device array of EXL3_STATIC_SCRATCH_BYTES (24 MiB), one per
  * GPU (zero-filled when the library is loaded, as a GEMV workspace's accumulators must
  * be), held until the process ends; a call whose exl3_gemv_grouped_workspace_bytes exceeds
  * it fails with EXL3_ERR_WORKSPACE (rows 1..4 fit every shape of the 27B model and its
@@ -146,7 +146,7 @@ int exl3_gemv_grouped(const void* A, const exl3_shard_t* shards, int nshards, vo
  * share the array and each leaves it ready for the next, so calls issued in order (one
  * stream, or graph replays in order) are safe; calls that may overlap in time race on it.
  */
-#define EXL3_STATIC_SCRATCH_BYTES (20u << 20)
+#define EXL3_STATIC_SCRATCH_BYTES (24u << 20)
 int exl3_gemv_grouped_static(const void* A, const exl3_shard_t* shards, int nshards, int rows, int ic,
                              void* stream);
 

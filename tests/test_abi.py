@@ -111,9 +111,9 @@ def test_workspace_sizes(native):
     arr = (native.Shard * 2)()
     arr[0].oc, arr[1].oc = 6144, 1024
     g = L.exl3_gemv_grouped_workspace_bytes(arr, 2, 4, 5120)
-    # the reserved 16 KiB head and the 2 MiB accumulator area lead every GEMV workspace once;
+    # the reserved 16 KiB head and the 6 MiB accumulator area lead every GEMV workspace once;
     # shards add their shares
-    head = 16384 + (2 << 20)
+    head = 16384 + (6 << 20)
     assert g == (L.exl3_gemv_workspace_bytes(4, 5120, 6144) + L.exl3_gemv_workspace_bytes(4, 5120, 1024)
                  - head)
     arr[0].oc = 100

@@ -111,7 +111,7 @@ def test_gemv1_workspace_head_untouched_and_deterministic(native):
     assert bool((ws[:16384] == 0xA5).all())
 
 
-ACC0, ACC1 = 16384, 16384 + (2 << 20)   # the workspace's accumulator area
+ACC0, ACC1 = 16384, 16384 + (6 << 20)   # the workspace's accumulator area
 
 
 @pytest.mark.parametrize("rows", [1, 3])

@@ -100,7 +100,7 @@ def test_static_lm_head_width_at_16_rows(native, oracle):
     print("static gemv: rows=16 lm_head 5120->151936 K=6", flush=True)
     y_static = torch.full((16, syn.VOCAB), float("nan"), dtype=torch.float16, device=dev)
     arr = _table(native, [lin], y_static, syn.VOCAB)
-    assert L.exl3_gemv_grouped_workspace_bytes(arr, 1, 16, syn.HIDDEN) <= (20 << 20)
+    assert L.exl3_gemv_grouped_workspace_bytes(arr, 1, 16, syn.HIDDEN) <= (24 << 20)
     rc = L.exl3_gemv_grouped_static(P(xd.data_ptr()), arr, 1, 16, syn.HIDDEN, stream)
     assert rc == 0, L.exl3_last_error().decode()
     y_ws = torch.full_like(y_static, float("nan"))
@@ -159,7 +159,7 @@ def test_static_rejects_calls_above_its_scratch(native):
     for i in range(4):
         arr[i] = native.Shard(0x10000, 0x10000, 0x10000, 0x10000, 4 * syn.INTERMEDIATE, syn.INTERMEDIATE, 4, 0)
     need = L.exl3_gemv_grouped_workspace_bytes(arr, 4, 16, syn.HIDDEN)
-    assert need > 16 << 20
+    assert need > 24 << 20
     rc = L.exl3_gemv_grouped_static(P(0x10000), arr, 4, 16, syn.HIDDEN, None)
     assert rc == 3
     msg = L.exl3_last_error().decode()
