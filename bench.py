@@ -261,7 +261,7 @@ def prefill_bench(reps: int) -> dict:
                             ("q 5120->6144 K4", 5120, 6144, 4)):
         d = _rand_linear(ic, oc, K, g, dev)
         row = {}
-        for M in (17, 40, 64, 80, 128, 144, 256, 384, 768, 1024, 2048, 4096):
+        for M in (17, 40, 64, 80, 128, 144, 256, 384, 768, 1024, 1536, 2048, 2560, 3072, 4096):
             x = torch.randn(M, ic, generator=g, device=dev).half()
             y = torch.empty(M, oc, dtype=torch.half, device=dev)
             row[M] = {"fused": t_of(lambda: _native.gemm(x, d["trellis"], d["suh"], d["svh"], K, 0, out=y)),
@@ -271,7 +271,7 @@ def prefill_bench(reps: int) -> dict:
                        ("gate_up (2 x 17408 K3)", [(17408, 3), (17408, 3)])):
         sh = [_rand_linear(5120, o, k, g, dev) for o, k in spec]
         row = {}
-        for M in (17, 64, 144):
+        for M in (17, 64, 144, 2048):
             x = torch.randn(M, 5120, generator=g, device=dev).half()
             row[M] = {"grouped": t_of(lambda: _native.gemm_grouped(x, sh)),
                       "per_shard_fused_cat": t_of(lambda: torch.cat(

@@ -306,8 +306,9 @@ class Exl3LinearMethod(LinearMethodBase):
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
         """fp16 activations through every shard, outputs side by side in slot order, cast
         back to x.dtype, plus bias (reference orcasaq2/config.py:228-245).  A fused layer at
-        <= GEMM_MAX_ROWS rows is one grouped op (decode-GEMV up to 16 rows, stream-K GEMM
-        above) that writes the concatenated output in place."""
+        <= GEMM_MAX_ROWS rows, or above it when every shard routes to the fused kernel, is one
+        grouped op (decode-GEMV up to 16 rows, stream-K GEMM above) that writes the
+        concatenated output in place."""
         if layer.exl3_shards is None:
             out = torch.nn.functional.linear(x, layer.exl3_dense.to(x.dtype))
             return out + bias if bias is not None else out
@@ -323,7 +324,8 @@ class Exl3LinearMethod(LinearMethodBase):
         if not xf.is_contiguous():
             xf = xf.contiguous()
         shards = layer.exl3_shards
-        if len(shards) > 1 and 0 < rows <= _ops.GEMM_MAX_ROWS:
+        if len(shards) > 1 and 0 < rows and (rows <= _ops.GEMM_MAX_ROWS or all(
+                _ops._fused_route(rows, xf.shape[-1], s.oc) for s in shards)):
             grouped = torch.ops.orcasaq2.shards_gemv if rows <= GEMV_MAX_ROWS else torch.ops.orcasaq2.shards_gemm
             out = grouped(
                 xf, [s.trellis for s in shards], [s.suh for s in shards], [s.svh for s in shards],

@@ -21,9 +21,12 @@ Dispatch on the number of activation rows (reference: orcasaq2/ops.py:25, 46-59)
                           reconstruct branch measured faster (_fused_gemm_faster);
   * rows > GEMM_MAX_ROWS  the reference's reconstruct branch: had_r_128(x, suh), dense W_q
                           (decoded transposed, (oc, ic)) into a scratch freed on exit, library
-                          fp16 transposed-B GEMM, had_r_128(y, svh) -- except shards of 8192+
-                          inputs up to WIDE_FUSED_MAX_ROWS rows (fused, measured faster) while
-                          the row knob is at its default.
+                          fp16 transposed-B GEMM, had_r_128(y, svh) -- except, while the row
+                          knob is at its default, the shapes where the fused kernel measured
+                          faster (_fused_gemm_faster: 8192+ inputs up to WIDE_FUSED_MAX_ROWS
+                          rows, 4096..8191 inputs with at least twice as many outputs in
+                          WIDE_OUT_FUSED_ROWS); a fused layer whose shards all route fused
+                          runs them as one grouped launch (shards_gemm).
 The op is registered for the "cuda" device type (ROCm) only: there is no CPU path.
 """
 
@@ -36,12 +39,13 @@ from . import _native
 
 # Rows at or below which the fused kernels are used (the reference's default and env knob,
 # orcasaq2/ops.py:22-25).  Above it the dense W_q is rebuilt once and a library GEMM runs --
-# except, while the knob is left at its default, for shards of 8192 or more inputs (down_proj)
-# up to WIDE_FUSED_MAX_ROWS rows, where the fused kernel measured faster (_fused_gemm_faster).
-# Setting the knob makes it the hard switch of the reference.
+# except, while the knob is left at its default, for the shapes where the fused kernel
+# measured faster (_fused_gemm_faster).  Setting the knob makes it the hard switch of the
+# reference.
 GEMM_MAX_ROWS = int(os.environ.get("ORCA_EXL3_GEMM_MAX_ROWS", "144"))
 GEMM_MAX_ROWS_SET = "ORCA_EXL3_GEMM_MAX_ROWS" in os.environ
-WIDE_FUSED_MAX_ROWS = 1024
+WIDE_FUSED_MAX_ROWS = 1536           # 8192+ inputs: fused up to here
+WIDE_OUT_FUSED_ROWS = (1536, 3072)   # 4096..8191 inputs, oc >= 2 ic: fused in (lo, hi] too
 GEMV_MAX_ROWS = _native.GEMV_MAX_ROWS
 
 
@@ -54,29 +58,35 @@ def exl3_K(trellis: Tensor):
 
 
 def _fused_gemm_faster(rows: int, ic: int, oc: int) -> bool:
-    """Whether the fused decode-GEMM beats the reconstruct branch for one shard at
-    GEMV_MAX_ROWS < rows <= GEMM_MAX_ROWS, or (ic >= 8192) at up to WIDE_FUSED_MAX_ROWS rows.
-    Measured on MI355X at settled clocks (us per call, HIP graph, fused / reconstruct branch):
-    17408 -> 5120 wins at every row count to 1024 (144 rows: 117 / 176, 256: 117 / 228, 1024:
-    224 / 310) and loses from 2048 (405 / 370); 5120 -> 17408 wins to 128 rows (79 / 85) and
-    loses at 144 (112 / 94); 5120 -> 6144 ties at 64 (47 / 46) and loses from 80 (60 / 49) to
-    144 (69 / 52).  With ic in [4096, 8192) the dense W_q is cheap to rebuild and the library
-    GEMM short, so above 64 rows the branch wins unless oc is at least twice ic and rows stay
-    within 128; other input widths (unmeasured below 4096) keep the fused path to
-    GEMM_MAX_ROWS."""
+    """Whether the fused decode-GEMM beats the reconstruct branch for one shard of `rows` >
+    GEMV_MAX_ROWS rows.  Measured on MI355X at settled clocks (us per call, HIP graph, fused /
+    reconstruct branch; the branch's library GEMM is far from monotone in the row count):
+      17408 -> 5120:  144: 116 / 176, 256: 118 / 225, 1024: 221 / 308, 1536: 308 / 430,
+                      2048: 397 / 373, 2560: 499 / 652, 3072: 589 / 487, 4096: 732 / 701;
+      5120 -> 17408:  64: 60 / 77, 128: 80 / 83, 144: 112 / 95, 384: 143 / 120,
+                      1024: 220 / 232, 1536: 300 / 285, 2048: 390 / 478, 2560: 478 / 569,
+                      3072: 592 / 644, 4096: 742 / 685;
+      5120 -> 6144:   40: 39 / 45, 64: 46 / 46, 80: 60 / 49, 144: 71 / 52, 2048: 166 / 142.
+    So: 8192+ inputs fused up to WIDE_FUSED_MAX_ROWS (the lone win at 2560 is not taken);
+    4096..8191 inputs fused up to 64 rows, and with oc >= 2 ic up to 128 rows and within
+    WIDE_OUT_FUSED_ROWS; narrower inputs (unmeasured below 4096) fused up to GEMM_MAX_ROWS."""
     if ic >= 8192:
         return rows <= WIDE_FUSED_MAX_ROWS
-    if rows <= 64 or ic < 4096:
+    if ic < 4096:
         return True
-    return rows <= 128 and oc >= 2 * ic
+    if oc >= 2 * ic:
+        lo, hi = WIDE_OUT_FUSED_ROWS
+        return rows <= 128 or lo < rows <= hi
+    return rows <= 64
 
 
 def _fused_route(rows: int, ic: int, oc: int) -> bool:
     """The fused decode-GEMM for rows > GEMV_MAX_ROWS: within GEMM_MAX_ROWS where it measured
-    faster, beyond it only for wide inputs while the knob is at its default."""
+    faster; beyond it, while the knob is at its default, for inputs of 4096 or more where it
+    measured faster (narrower inputs keep the reference's switch)."""
     if rows <= GEMM_MAX_ROWS:
         return _fused_gemm_faster(rows, ic, oc)
-    return not GEMM_MAX_ROWS_SET and ic >= 8192 and _fused_gemm_faster(rows, ic, oc)
+    return not GEMM_MAX_ROWS_SET and ic >= 4096 and _fused_gemm_faster(rows, ic, oc)
 
 
 def _shard_gemm_impl(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, oc: int, k: float,
@@ -132,10 +142,11 @@ def _shards_gemv_fake(x, trellis, suh, svh, oc, k, mcg, mul1) -> Tensor:
 @torch.library.custom_op("orcasaq2::shards_gemm", mutates_args=(), device_types="cuda")
 def shards_gemm(x: Tensor, trellis: list[Tensor], suh: list[Tensor], svh: list[Tensor],
                 oc: list[int], k: list[float], mcg: list[bool], mul1: list[bool]) -> Tensor:
-    """All shards of a fused layer for 16 < rows <= GEMM_MAX_ROWS: one set-up kernel (each
-    shard's Hadamard pass) and one stream-K launch per codebook for all of them, outputs
-    side by side -- the per-shard shard_gemm loop + torch.cat of orcasaq2/config.py:237-243
-    with one launch tail instead of one per shard."""
+    """All shards of a fused layer for rows > 16 (up to GEMM_MAX_ROWS, and above it when every
+    shard routes fused): one set-up kernel (each shard's Hadamard pass) and one stream-K
+    launch per codebook (per K with 256-row tiles) for all of them, outputs side by side --
+    the per-shard shard_gemm loop + torch.cat of orcasaq2/config.py:237-243 with one launch
+    tail instead of one per shard."""
     shards = [dict(trellis=t, suh=a, svh=b, oc=o, K=kk, codebook=_native.codebook_id(m, m1))
               for t, a, b, o, kk, m, m1 in zip(trellis, suh, svh, oc, k, mcg, mul1)]
     return _native.gemm_grouped(x, shards)

@@ -58,7 +58,7 @@ def test_shard_gemm_routing_by_shape(native, oracle, rows, oc):
     2 ic, or more than 128 rows), the fused GEMM for wide outputs up to 128 rows; both match
     the oracle."""
     ic = 5120
-    assert O._fused_gemm_faster(rows, ic, oc) == (oc >= 2 * ic and rows <= 128)
+    assert O._fused_gemm_faster(rows, ic, oc) == (oc >= 2 * ic and rows <= 128)   # within GEMM_MAX_ROWS
     lin = syn.linear(ic, oc, 3, seed=rows + oc)
     x = syn.activations(rows, ic, torch.Generator().manual_seed(rows))
     d = on(lin)
@@ -104,8 +104,9 @@ def _two_shard_step(rows, ic=1024):
 def test_hip_graph_capture_replays(native, oracle, rows):
     """The op and the grouped op captured into a HIP graph on a stream that ran them eagerly
     first (so the capture uses that stream's eager GEMV workspace), replayed four times with
-    eager work between replays, against eager results: 1 row (persistent decode launch and
-    its split-segment finishing kernel), 2 rows (four-row template), 9 rows (the 5..16-row
+    eager work between replays, against eager results: 1 row (persistent decode launch that
+    finishes its split column groups through the accumulator area), 2 rows (four-row
+    template), 9 rows (the 5..16-row
     kernel: set-up, one decode launch over both K, finish), 40 rows (prefill: 48-row stream-K tiles, counters zeroed by the
     set-up kernels inside the graph)."""
     step = _two_shard_step(rows)
@@ -234,8 +235,8 @@ def test_torch_compile_treats_op_as_opaque(native):
 
 def test_linear_method_apply_fused_layers(native, oracle):
     """qkv_proj-style layer: shards captured by slot, processed, applied (grouped decode-GEMV
-    at <= 16 rows, grouped GEMM to 144, per-shard ops + cat above), bias added, dtype
-    restored."""
+    at <= 16 rows, grouped GEMM to 144, per-shard ops + cat above for these narrow inputs),
+    bias added, dtype restored."""
     from orcasaq2.config import Exl3Config, Exl3LinearMethod
     from orcasaq2._vllm_compat import LinearBase
     cfg = Exl3Config.from_config({"bits": 4})
@@ -263,6 +264,45 @@ def test_linear_method_apply_fused_layers(native, oracle):
             err = np.linalg.norm(got - want, axis=1) / np.linalg.norm(want, axis=1)
             assert err.max() < 1e-2, (sid, rows, err.max())  # bf16 output rounding
             col += oc
+
+
+def test_linear_method_apply_grouped_above_gemm_max_rows(native, oracle):
+    """A gate_up-style layer (4096 inputs, two 8192-output shards, K = 3 and 4) at 2048 rows:
+    above GEMM_MAX_ROWS every shard routes to the fused GEMM (oc >= 2 ic inside
+    WIDE_OUT_FUSED_ROWS), so apply runs them as one grouped launch -- bit for bit the
+    grouped op's output -- and sampled rows of both shards match the oracle."""
+    from orcasaq2.config import Exl3Config
+    from orcasaq2._vllm_compat import LinearBase
+    if O.GEMM_MAX_ROWS_SET:
+        pytest.skip("the row knob is set: the reference's hard switch applies")
+    rows, ic = 2048, 4096
+    spec = [(0, 8192, 3), (1, 8192, 4)]
+    assert all(O._fused_route(rows, ic, oc) for _, oc, _ in spec)
+    lins = {sid: syn.linear(ic, oc, K, seed=40 + sid) for sid, oc, K in spec}
+    cfg = Exl3Config.from_config({"bits": 4})
+    layer = LinearBase(ic, 2 * 8192, bias=False, params_dtype=torch.float16, quant_config=cfg,
+                       prefix="model.layers.0.mlp.gate_up_proj", output_partition_sizes=[8192, 8192])
+    for sid, _, _ in spec:
+        for name in ("trellis", "suh", "svh"):
+            p = getattr(layer, name)
+            p.weight_loader(p, lins[sid][name].to(D), sid)
+    layer.quant_method.process_weights_after_loading(layer)
+    x = syn.activations(rows, ic, torch.Generator().manual_seed(41))
+    print(f"apply gate_up-like 4096 -> 2 x 8192 rows={rows}", flush=True)
+    y = layer(x.to(D))
+    sh = layer.exl3_shards
+    yg = torch.ops.orcasaq2.shards_gemm(x.to(D), [s.trellis for s in sh], [s.suh for s in sh], [s.svh for s in sh],
+                                        [s.oc for s in sh], [float(s.K) for s in sh], [False, False], [False, False])
+    assert torch.equal(y, yg)
+    idx = torch.tensor([0, 1, 255, 256, 1027, rows - 1])
+    col = 0
+    for sid, oc, K in spec:
+        l = lins[sid]
+        W = oracle.reconstruct_f16(l["trellis"], K, 0)
+        want = oracle.shard_gemm_ref(x[idx].numpy(), l["trellis"], l["suh"].numpy(), l["svh"].numpy(), K, 0, W=W)
+        got = y[idx.to(D), col:col + oc].cpu().numpy()
+        assert oracle.rel_err_rows(got, want).max() <= 1e-3, sid
+        col += oc
 
 
 def test_embedding_method_int8_on_gpu(native):
