@@ -87,6 +87,10 @@ __device__ __forceinline__ void g16_body(const G1Group& a, const G16Shard* sht, 
     long lw = g16_lane_word(lane, g16_sh<ONE>(sht, pf.s).oc16, K);
     int lw_s = pf.s;
     int jpf = 0;
+    // Lane 16 j + i holds activation row i of the A operand.  Rows past the call's nrows only
+    // feed C rows that are never stored, so their lanes read the last live row's fragment:
+    // at up to 8 rows a k-group's 16 lanes then touch one 128-byte line instead of two.
+    const int lane_a = g16_ah_lane(lane, a.nrows);
     auto load = [&](G16Unit<K>& u, const G16Cursor& c) {
         if (c.s != lw_s) {
             lw_s = c.s;
@@ -94,7 +98,7 @@ __device__ __forceinline__ void g16_body(const G1Group& a, const G16Shard* sht, 
         }
         g16_load<K>(u.w, c.p + lw);
 #pragma unroll
-        for (int m = 0; m < 4; m++) u.a[m] = *reinterpret_cast<const uint4*>(c.ah + g16_ah_word(m, lane));
+        for (int m = 0; m < 4; m++) u.a[m] = *reinterpret_cast<const uint4*>(c.ah + g16_ah_word(m, lane_a));
     };
     G16Unit<K> un;
     if (n > 0) load(un, pf);

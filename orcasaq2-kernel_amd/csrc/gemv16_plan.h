@@ -193,6 +193,15 @@ G1_HD int g16_ah_word(int m, int lane)
     return (m * 64 + lane) * 4;
 }
 
+// The lane whose A fragment lane l reads when the call has nrows rows: lane 16 j + i holds
+// activation row i, and a row past nrows (written by no set-up wave; its C row is never
+// stored) reads row nrows - 1 of the same k-group instead.
+G1_HD int g16_ah_lane(int lane, int nrows)
+{
+    const int i = lane & 15;
+    return (lane & ~15) | (i < nrows ? i : nrows - 1);
+}
+
 // Where the set-up kernel puts input k (of ic) of activation row i: u32 offset in the shard's
 // fragments (duplicated fp16 pair).  k = 64 q + 16 j + rr, rr = 2 m + o, o in {0, 1, 8, 9} at
 // slot t = o % 2 + 2 (o / 8); lane 16 j + i of step m reads slots 0..3.

@@ -1013,17 +1013,22 @@ void g16_replay_wg(G16World& W, const GemvShard* shards, const G1Group& a, const
                 const long wd = off_of(p) / 4, tile = wd / (8 * K), ti = tile / e.oc16, tj = tile % e.oc16;
                 if (ti != 4 * c.q + (lane >> 4) || tj != 2 * c.strip + ((lane & 15) >> 3) || (wd % (8 * K)) != (lane & 7) * K)
                     fail("gemv16 lane %d loads tile (%ld, %ld) word %ld", lane, ti, tj, wd % (8 * K));
+                // a live row's lane reads its own row; a dead row's lane the last live row
+                const int lane_a = g16_ah_lane(lane, a.nrows);
+                if ((lane_a >> 4) != (lane >> 4)) fail("gemv16 lane %d reads k-group of lane %d", lane, lane_a);
+                if ((lane & 15) < a.nrows ? lane_a != lane : (lane_a & 15) != a.nrows - 1)
+                    fail("gemv16 lane %d reads the fragment of lane %d at %d rows", lane, lane_a, a.nrows);
                 for (int m = 0; m < 4; m++) {
-                    const uint32_t* ap = c.ah + g16_ah_word(m, lane);
+                    const uint32_t* ap = c.ah + g16_ah_word(m, lane_a);
                     need_in(ap, 16, B_WS, W.ah_off[gi] + g16_ah_words(W.ic) * 4, "gemv16 fragment load");
                     const long rel = (off_of(ap) - W.ah_off[gi]) / 4;
                     if (rel < 0) fail("gemv16 fragment load before the shard's fragments");
                     // the four words are row i's inputs 64 q + 16 j + 2 m + {0, 1, 8, 9}
-                    const int i = lane & 15, j = lane >> 4;
+                    const int i = lane_a & 15, j = lane >> 4;
                     const int o[4] = {0, 1, 8, 9};
                     for (int t = 0; t < 4; t++) {
                         if (g16_ah_elem(i, 64 * c.q + 16 * j + 2 * m + o[t]) != rel + t) fail("gemv16 fragment word of the wrong input");
-                        if (i < a.nrows && !W.ah_written[gi][rel + t]) fail("gemv16 reads a fragment word the set-up did not write");
+                        if (!W.ah_written[gi][rel + t]) fail("gemv16 reads a fragment word the set-up did not write");
                     }
                 }
             }
