@@ -11,7 +11,8 @@
 // 16 rows for the same decode work (the unit layout is in gemv16_plan.h).  A 16-row
 // activation table would not fit in LDS, so a set-up kernel writes every shard's transformed
 // activations fp16(H128(x_r * suh)) once per call in the A-fragment order, and each lane loads
-// its 16-byte fragments of a unit from there (L2-resident: 64 KB per 1024 inputs per shard).
+// its 8-byte fragments of a unit from there (L2-resident: 32 KB per 1024 inputs per shard) and
+// duplicates each input into the two k-slots that meet a masked word's halves.
 //
 // Work decomposition as in gemv1.hip: units numbered shard, strip (32 outputs), then unit
 // down the strip; G nearly equal contiguous ranges, one per workgroup of 8 waves (at odd K a
@@ -64,10 +65,18 @@ __device__ __forceinline__ void g16_mfma(const uint32_t (&w)[K + 1], const uint4
                                                     acc[H], 0, 0, 0);
 }
 
+// A fragment of four fp16 inputs (two words) as the MFMA's eight k-slots: each input in the
+// two slots that meet a masked word's two halves.
+__device__ __forceinline__ uint4 g16_dup(const uint2 x)
+{
+    return uint4{__builtin_amdgcn_perm(x.x, x.x, 0x01000100u), __builtin_amdgcn_perm(x.x, x.x, 0x03020302u),
+                 __builtin_amdgcn_perm(x.y, x.y, 0x01000100u), __builtin_amdgcn_perm(x.y, x.y, 0x03020302u)};
+}
+
 template <int K>
 struct G16Unit {
     uint32_t w[K + 1];
-    uint4 a[4];
+    uint2 a[4];   // four fp16 inputs per MFMA step, duplicated when the step runs
 };
 
 // Workgroup g of group a (shard table sht) -- the whole decode kernel body.
@@ -98,7 +107,7 @@ __device__ __forceinline__ void g16_body(const G1Group& a, const G16Shard* sht, 
         }
         g16_load<K>(u.w, c.p + lw);
 #pragma unroll
-        for (int m = 0; m < 4; m++) u.a[m] = *reinterpret_cast<const uint4*>(c.ah + g16_ah_word(m, lane_a));
+        for (int m = 0; m < 4; m++) u.a[m] = *reinterpret_cast<const uint2*>(c.ah + g16_ah_word(m, lane_a));
     };
     G16Unit<K> un;
     if (n > 0) load(un, pf);
@@ -123,14 +132,26 @@ __device__ __forceinline__ void g16_body(const G1Group& a, const G16Shard* sht, 
         if (j + 1 < n) g16_advance<K, ONE>(a, sht, cu);
         g16_next_pf<K, ONE>(a, sht, pf, jpf, n);
         load(un, pf);
-        g16_mfma<K, CB, 0, 0>(u.w, u.a[0], acc, kc);
-        g16_mfma<K, CB, 0, 1>(u.w, u.a[0], acc, kc);
-        g16_mfma<K, CB, 1, 0>(u.w, u.a[1], acc, kc);
-        g16_mfma<K, CB, 1, 1>(u.w, u.a[1], acc, kc);
-        g16_mfma<K, CB, 2, 0>(u.w, u.a[2], acc, kc);
-        g16_mfma<K, CB, 2, 1>(u.w, u.a[2], acc, kc);
-        g16_mfma<K, CB, 3, 0>(u.w, u.a[3], acc, kc);
-        g16_mfma<K, CB, 3, 1>(u.w, u.a[3], acc, kc);
+        {
+            const uint4 a0 = g16_dup(u.a[0]);
+            g16_mfma<K, CB, 0, 0>(u.w, a0, acc, kc);
+            g16_mfma<K, CB, 0, 1>(u.w, a0, acc, kc);
+        }
+        {
+            const uint4 a1 = g16_dup(u.a[1]);
+            g16_mfma<K, CB, 1, 0>(u.w, a1, acc, kc);
+            g16_mfma<K, CB, 1, 1>(u.w, a1, acc, kc);
+        }
+        {
+            const uint4 a2 = g16_dup(u.a[2]);
+            g16_mfma<K, CB, 2, 0>(u.w, a2, acc, kc);
+            g16_mfma<K, CB, 2, 1>(u.w, a2, acc, kc);
+        }
+        {
+            const uint4 a3 = g16_dup(u.a[3]);
+            g16_mfma<K, CB, 3, 0>(u.w, a3, acc, kc);
+            g16_mfma<K, CB, 3, 1>(u.w, a3, acc, kc);
+        }
         const int done = j + 1;
         if (done == pq1) __builtin_amdgcn_s_setprio(2);
         if (done == pq2) __builtin_amdgcn_s_setprio(1);
@@ -255,7 +276,7 @@ __global__ __launch_bounds__(256) void gemv16_finish_multi_kernel(const G16Multi
 }
 
 // One wave per (shard, row, 128-input block): fp16(H128(A_r * suh_s)) into the shard's
-// fragments (lane l: inputs 2l, 2l + 1, one duplicated pair each, adjacent words).
+// fragments (lane l: inputs 2l, 2l + 1, the two halves of one word).
 __global__ __launch_bounds__(256) void gemv16_prep_kernel(const G16Prep p)
 {
     const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -271,7 +292,7 @@ __global__ __launch_bounds__(256) void gemv16_prep_kernel(const G16Prep p)
                (float)__builtin_bit_cast(_Float16, (uint16_t)(sw >> 16));
     wave_fwht128(v0, v1);
     const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)v0), h1 = __builtin_bit_cast(uint16_t, (_Float16)v1);
-    *reinterpret_cast<uint2*>(p.ah[s] + g16_ah_elem(r, b * 128 + 2 * lane)) = uint2{h0 | (h0 << 16), h1 | (h1 << 16)};
+    reinterpret_cast<uint32_t*>(p.ah[s])[g16_ah_elem(r, b * 128 + 2 * lane) >> 1] = h0 | (h1 << 16);
 }
 
 // ---------------------------------------------------------------- host side

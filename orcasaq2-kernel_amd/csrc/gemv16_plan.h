@@ -14,8 +14,9 @@ namespace exl3 {
 constexpr int G16_ROWS = 16;             // activation rows of an MFMA (rows >= nrows unused)
 constexpr int G16_STRIP = 32;            // outputs of a strip (two tile columns)
 constexpr int G16_QIN = 64;              // inputs of a unit (four tile rows)
-// Words (u32) of one unit's activation fragments: 4 MFMA steps m x 64 lanes x 4 u32.
-constexpr int G16_AH_UNIT = 4 * 64 * 4;
+// Words (u32) of one unit's activation fragments: 4 MFMA steps m x 64 lanes x 2 u32 (four
+// fp16 inputs, each duplicated into its two k-slots in registers).
+constexpr int G16_AH_UNIT = 4 * 64 * 2;
 
 // A unit is 4 tile rows x 2 tile columns (64 inputs x 32 outputs, 8 tiles, 64 chunks): lane
 // l = 16 j + n decodes chunk c = n % 8 of tile (tile row 4 q + j, tile column 2 strip + n / 8),
@@ -23,7 +24,7 @@ constexpr int G16_AH_UNIT = 4 * 64 * 4;
 // positions 8 m + 4 h + t (t = 0..3) of every lane's chunk -- tile rows 2 m + {0, 1, 8, 9}[t]
 // of column c + 8 h -- as B (each masked word's two fp16 halves as two k-slots), and as A the
 // matching inputs of all 16 activation rows, each duplicated: A row i, k-group j holds row i's
-// inputs 64 q + 16 j + 2 m + {0, 1, 8, 9}.  C column n of MFMA (m, h) is output
+// inputs 64 q + 16 j + 2 m + {0, 1, 8, 9} (stored once each, duplicated when loaded).  C column n of MFMA (m, h) is output
 // 16 (n / 8) + n % 8 + 8 h of the strip; the four m accumulate into the same C.
 struct G16Shard {
     const uint32_t* trellis;   // (ic/16, oc/16, 8K) u32
@@ -187,10 +188,11 @@ G1_HD int g16_block_wg(int b, int n, int K)
     return x * base + (x < rem ? x : rem) + y;
 }
 
-// u32 offset of lane l's A fragment of MFMA step m in a unit's activation fragments.
+// u32 offset of lane l's A fragment of MFMA step m in a unit's activation fragments (two
+// words: slots 0, 1 and slots 2, 3, one fp16 input per slot).
 G1_HD int g16_ah_word(int m, int lane)
 {
-    return (m * 64 + lane) * 4;
+    return (m * 64 + lane) * 2;
 }
 
 // The lane whose A fragment lane l reads when the call has nrows rows: lane 16 j + i holds
@@ -202,14 +204,15 @@ G1_HD int g16_ah_lane(int lane, int nrows)
     return (lane & ~15) | (i < nrows ? i : nrows - 1);
 }
 
-// Where the set-up kernel puts input k (of ic) of activation row i: u32 offset in the shard's
-// fragments (duplicated fp16 pair).  k = 64 q + 16 j + rr, rr = 2 m + o, o in {0, 1, 8, 9} at
-// slot t = o % 2 + 2 (o / 8); lane 16 j + i of step m reads slots 0..3.
+// Where the set-up kernel puts input k (of ic) of activation row i: fp16 (u16) offset in the
+// shard's fragments.  k = 64 q + 16 j + rr, rr = 2 m + o, o in {0, 1, 8, 9} at slot
+// t = o % 2 + 2 (o / 8); lane 16 j + i of step m reads slots 0..3 (u16 2 w + t of its words),
+// so inputs k and k + 1 (k even) share one u32.
 G1_HD long g16_ah_elem(int i, int k)
 {
     const int q = k >> 6, j = (k >> 4) & 3, rr = k & 15;
     const int m = (rr & 7) >> 1, t = (rr & 1) + 2 * (rr >> 3);
-    return (long)q * G16_AH_UNIT + g16_ah_word(m, 16 * j + i) + t;
+    return 2 * ((long)q * G16_AH_UNIT + g16_ah_word(m, 16 * j + i)) + t;
 }
 
 // u32 words of one shard's activation fragments.

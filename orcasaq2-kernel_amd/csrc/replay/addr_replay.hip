@@ -973,12 +973,12 @@ void g16_replay_prep(G16World& W, const G16Prep& p)
         for (int lane = 0; lane < 64; lane++) {
             need_in(reinterpret_cast<const uint32_t*>(p.A + (long)r * p.ic + b * 128) + lane, 4, B_X, (long)W.rows * W.ic * 2, "A load (set-up)");
             need_in(reinterpret_cast<const uint32_t*>(p.suh[s] + b * 128) + lane, 4, B_SUH + s, (long)W.ic * 2, "suh load (set-up)");
+            // inputs 2 lane and 2 lane + 1 of the block: the two halves of one word
             const long e = g16_ah_elem(r, b * 128 + 2 * lane);
-            if (e < 0 || e + 2 > words || (e & 1)) fail("fragment store %ld of %ld", e, words);
-            for (int t = 0; t < 2; t++) {
-                if (W.ah_written[s][e + t]) fail("fragment word %ld of shard %d written twice", e + t, s);
-                W.ah_written[s][e + t] = 1;
-            }
+            if (e < 0 || e + 2 > 2 * words || (e & 1)) fail("fragment store at half %ld of %ld", e, 2 * words);
+            if (g16_ah_elem(r, b * 128 + 2 * lane + 1) != e + 1) fail("fragment inputs %d, %d not one word", b * 128 + 2 * lane, b * 128 + 2 * lane + 1);
+            if (W.ah_written[s][e >> 1]) fail("fragment word %ld of shard %d written twice", e >> 1, s);
+            W.ah_written[s][e >> 1] = 1;
         }
     }
 }
@@ -1020,15 +1020,16 @@ void g16_replay_wg(G16World& W, const GemvShard* shards, const G1Group& a, const
                     fail("gemv16 lane %d reads the fragment of lane %d at %d rows", lane, lane_a, a.nrows);
                 for (int m = 0; m < 4; m++) {
                     const uint32_t* ap = c.ah + g16_ah_word(m, lane_a);
-                    need_in(ap, 16, B_WS, W.ah_off[gi] + g16_ah_words(W.ic) * 4, "gemv16 fragment load");
+                    need_in(ap, 8, B_WS, W.ah_off[gi] + g16_ah_words(W.ic) * 4, "gemv16 fragment load");
+                    if (off_of(ap) & 7) fail("gemv16 fragment load not 8-byte aligned");
                     const long rel = (off_of(ap) - W.ah_off[gi]) / 4;
                     if (rel < 0) fail("gemv16 fragment load before the shard's fragments");
-                    // the four words are row i's inputs 64 q + 16 j + 2 m + {0, 1, 8, 9}
+                    // the two words' four halves are row i's inputs 64 q + 16 j + 2 m + {0, 1, 8, 9}
                     const int i = lane_a & 15, j = lane >> 4;
                     const int o[4] = {0, 1, 8, 9};
                     for (int t = 0; t < 4; t++) {
-                        if (g16_ah_elem(i, 64 * c.q + 16 * j + 2 * m + o[t]) != rel + t) fail("gemv16 fragment word of the wrong input");
-                        if (!W.ah_written[gi][rel + t]) fail("gemv16 reads a fragment word the set-up did not write");
+                        if (g16_ah_elem(i, 64 * c.q + 16 * j + 2 * m + o[t]) != 2 * rel + t) fail("gemv16 fragment half of the wrong input");
+                        if (!W.ah_written[gi][rel + t / 2]) fail("gemv16 reads a fragment word the set-up did not write");
                     }
                 }
             }
