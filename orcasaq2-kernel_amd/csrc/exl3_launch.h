@@ -59,7 +59,7 @@ int gemv16_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int
                     hipStream_t stream);
 size_t gemm_grouped_shard_bytes(int rows, int ic, int oc);
 int gemm_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws,
-                          size_t ws_bytes, hipStream_t stream);
+                          size_t ws_bytes, hipStream_t stream, const char* what = "exl3_gemm_grouped");
 int gemm_sk_cus();
 int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
                      size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream);

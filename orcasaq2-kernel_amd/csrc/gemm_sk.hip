@@ -811,11 +811,11 @@ static int sk_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int n
                                [&](const SkLaunch& L) { return sk_emit(L, what, stream); });
 }
 
-// Prefill of several shards (exl3_gemm_grouped): tile height by rows, as for one shard.
+// Prefill of several shards (exl3_gemm_grouped; exl3_gemm's one-shard form at few rows):
+// tile height by rows, as for one shard.  `what` names the entry point in errors.
 int gemm_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws,
-                          size_t ws_bytes, hipStream_t stream)
+                          size_t ws_bytes, hipStream_t stream, const char* what)
 {
-    const char* what = "exl3_gemm_grouped";
     switch (gemm_sk_bm(rows)) {
     case 32: return sk_grouped_dispatch<32>(A, shards, nshards, rows, ws, ws_bytes, what, stream);
     case 48: return sk_grouped_dispatch<48>(A, shards, nshards, rows, ws, ws_bytes, what, stream);

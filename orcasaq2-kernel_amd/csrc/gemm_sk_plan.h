@@ -259,6 +259,9 @@ SK_HD int sk_cx(int row, int col) { return row * (SK_BN + 4) + col; }
 
 inline size_t sk_align(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// exl3_gemm's Hadamard output fp16(H(A * suh)) at the head of its workspace.
+inline size_t gemm_sk_ah_bytes(int rows, int ic) { return sk_align((size_t)rows * ic * 2); }
+
 // Workgroups per launch: one per CU, all resident at once.
 template <int BM>
 inline int sk_gmax(int cus) { return cus; }
@@ -271,6 +274,11 @@ inline int sk_ntn(int oc) { return (oc + SK_BN - 1) / SK_BN; }
 // Counters and slots of one launch of `tiles` tiles and up to G workgroups.
 template <int BM>
 inline size_t sk_ws(long tiles, int G) { return sk_align((size_t)tiles * 4) + (size_t)(tiles + G) * sk_slot_bytes<BM>(); }
+
+// exl3_gemm up to this many rows runs as the one-shard grouped launch (its set-up kernel does
+// the Hadamard pass and the counter clear in one launch); above, a Hadamard pass of its own,
+// the counter clear and the stream-K kernel.  The workspace layout is the same.
+constexpr int SK_PREP_MAX_ROWS = 384;
 
 // Tile height of a prefill launch of `rows` rows.  Each weight is decoded once per row tile;
 // a taller tile pays that decode over more rows but MFMA work for padding rows and bigger

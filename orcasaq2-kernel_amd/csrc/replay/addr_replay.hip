@@ -1193,7 +1193,8 @@ int exl3r_gemv1(int rows, int ic, int nshards, const int* oc, const int* K, cons
 }
 
 
-// The stream-K GEMM for nshards shards sharing ic: mode 0 = exl3_gemm (one shard), 1 =
+// The stream-K GEMM for nshards shards sharing ic: mode 0 = exl3_gemm (one shard; up to
+// SK_PREP_MAX_ROWS rows it is the one-shard grouped plan, as gemm_dispatch runs it), 1 =
 // exl3_gemm_grouped; tile height by rows.  Workspaces are sized as the product sizes them for
 // `cus` CUs.  Returns as exl3r_gemv1; stats: launches, K-step loads checked, pieces, slot
 // stores.
@@ -1204,6 +1205,16 @@ int exl3r_gemm_sk(int mode, int rows, int ic, int nshards, const int* oc, const 
     try {
         if (nshards < 1 || nshards > EXL3_MAX_SHARDS || (mode == 0 && nshards != 1) || mode < 0 || mode > 1)
             fail("mode %d, nshards %d", mode, nshards);
+        if (mode == 0 && rows <= SK_PREP_MAX_ROWS) {
+            // exl3_gemm's workspace (its Hadamard output, then counters and slots) is exactly
+            // the one-shard grouped launch's
+            if (gemm_sk_ah_bytes(rows, ic) + sk_single_bytes(rows, oc[0], cus) !=
+                sk_grouped_bytes_bm(gemm_sk_bm(rows), rows, ic, oc[0], cus))
+                fail("exl3_gemm workspace %zu != one-shard grouped workspace %zu",
+                     gemm_sk_ah_bytes(rows, ic) + sk_single_bytes(rows, oc[0], cus),
+                     sk_grouped_bytes_bm(gemm_sk_bm(rows), rows, ic, oc[0], cus));
+            mode = 1;
+        }
         SkWorld W;
         W.rows = rows;
         W.ic = ic;
