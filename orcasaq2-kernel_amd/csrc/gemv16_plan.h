@@ -339,8 +339,14 @@ inline int g16_place(G1Group& grp, long U, int G, char* slots, size_t& sbase, si
     return EXL3_OK;
 }
 
-// Workgroup counts of one launch: G1_UNITS_PER_WG units each, up to G1_WG_PER_CU workgroups per
-// CU resident, shared in proportion to the groups' sizes.  Where that leaves a range so long
+// Units per workgroup the 5..16-row plan aims for (the batch-1 plan's G1_UNITS_PER_WG is 32):
+// with fewer, a mid-size layer still fills every CU with G1_WG_PER_CU workgroups (qkv at 16
+// rows: 640 -> 1024 workgroups, 21.3-21.8 -> 20.8 us per call on MI355X; gate_up and the
+// lm_head are capped at G1_WG_PER_CU per CU either way and did not change).
+constexpr int G16_UNITS_PER_WG = 16;
+
+// Workgroup counts of one launch: G16_UNITS_PER_WG units each, up to G1_WG_PER_CU workgroups
+// per CU resident, shared in proportion to the groups' sizes.  Where that leaves a range so long
 // that its partial strips would not let G1_WG_PER_CU workgroups share a CU (few CUs, very large
 // shards), a group takes more workgroups than stay resident (no workgroup waits for another).
 inline void g16_split(const long* U, int ns, int nq, int cus, int* G, size_t& lds)
@@ -348,7 +354,7 @@ inline void g16_split(const long* U, int ns, int nq, int cus, int* G, size_t& ld
     const int gmax = std::min(G1_GMAX, G1_WG_PER_CU * cus);
     long Gsum = 0;
     for (int t = 0; t < ns; t++) {
-        G[t] = (int)std::min<long>(gmax, std::max<long>(1, U[t] / G1_UNITS_PER_WG));
+        G[t] = (int)std::min<long>(gmax, std::max<long>(1, U[t] / G16_UNITS_PER_WG));
         Gsum += G[t];
     }
     if (Gsum > gmax)
