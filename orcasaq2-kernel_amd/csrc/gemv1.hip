@@ -17,7 +17,8 @@
 //      for every row r, into an LDS table of duplicated fp16 pairs; then each wave issues the
 //      loads of its first unit;
 //   2. main loop over the run: each unit's loads are issued in the previous unit's
-//      iteration (g1_depth: one unit in flight per wave, eight waves per SIMD).
+//      iteration (D = g1_depth: one unit in flight per wave, eight waves per SIMD; two for
+//      the four-row template when the launch's LDS leaves fewer workgroups resident).
 //      The tail-biting word before a lane's chunk is the previous lane's last word (DPP
 //      rotate within the tile's 8 lanes).  Each position is decoded with three VALU ops
 //      (dot2_word); the masked words go into the B operand of v_mfma_f32_16x16x32_f16
@@ -177,11 +178,10 @@ __device__ __forceinline__ uint32_t g1_dup(float v)
 // Workgroup g of group a (shard table sht) -- the whole kernel body.  The range, cursor,
 // occurrence, LDS and global index arithmetic is gemv1_plan.h's (shared with the CPU address
 // replay).
-template <int K, int CB, bool ONE, int R>
+template <int K, int CB, bool ONE, int R, int D>
 __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, const int g, uint32_t* lds)
 {
     auto sh = [&](int s) -> const G1Shard& { return g1_sh<ONE>(sht, s); };
-    constexpr int D = g1_depth(K);
 
     const G1Range w = g1_range<ONE>(a, sht, g);
     const int nr = R == 1 ? 1 : a.nrows;     // activation rows in the tables and results
@@ -197,7 +197,6 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
 
     // A unit's loads: the lane's K words.  Prefetch cursor (D units ahead; it stops at the
     // wave's last unit, whose data is then loaded again and not used) and processing cursor.
-    // D = g1_depth(K) = 1 on MI355X; the ring stays general.
     struct Slot {
         uint32_t w[K + 1];
     };
@@ -370,12 +369,20 @@ template <int K, int CB, bool ONE, int R>
 __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8), amdgpu_num_sgpr(74))) void gemv1_kernel(const G1Args a)
 {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-    g1_body<K, CB, ONE, R>(a.grp, a.sh, blockIdx.x, lds);
+    g1_body<K, CB, ONE, R, 1>(a.grp, a.sh, blockIdx.x, lds);
+}
+
+// The four-row template with G1_DEEP units in flight per wave (g1_depth).
+template <int K, int CB, bool ONE>
+__global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8), amdgpu_num_sgpr(74))) void gemv1_deep_kernel(const G1Args a)
+{
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    g1_body<K, CB, ONE, G1_ROWS, G1_DEEP>(a.grp, a.sh, blockIdx.x, lds);
 }
 
 // Several groups (different K) in one launch: their start-up and reduction tails overlap
 // instead of following each other.
-template <int CB, int R>
+template <int CB, int R, int D = 1>
 __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8), amdgpu_num_sgpr(74))) void gemv1_multi_kernel(const G1Multi)
 {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
@@ -388,14 +395,14 @@ __global__ __launch_bounds__(64 * G1_NW) __attribute__((amdgpu_waves_per_eu(8, 8
     const G1Shard* sht = mm.sh + mm.sh0[i];
     const int g = blockIdx.x - mm.gbeg[i];
     switch (mm.K[i]) {
-    case 1: g1_body<1, CB, false, R>(a, sht, g, lds); break;
-    case 2: g1_body<2, CB, false, R>(a, sht, g, lds); break;
-    case 3: g1_body<3, CB, false, R>(a, sht, g, lds); break;
-    case 4: g1_body<4, CB, false, R>(a, sht, g, lds); break;
-    case 5: g1_body<5, CB, false, R>(a, sht, g, lds); break;
-    case 6: g1_body<6, CB, false, R>(a, sht, g, lds); break;
-    case 7: g1_body<7, CB, false, R>(a, sht, g, lds); break;
-    case 8: g1_body<8, CB, false, R>(a, sht, g, lds); break;
+    case 1: g1_body<1, CB, false, R, D>(a, sht, g, lds); break;
+    case 2: g1_body<2, CB, false, R, D>(a, sht, g, lds); break;
+    case 3: g1_body<3, CB, false, R, D>(a, sht, g, lds); break;
+    case 4: g1_body<4, CB, false, R, D>(a, sht, g, lds); break;
+    case 5: g1_body<5, CB, false, R, D>(a, sht, g, lds); break;
+    case 6: g1_body<6, CB, false, R, D>(a, sht, g, lds); break;
+    case 7: g1_body<7, CB, false, R, D>(a, sht, g, lds); break;
+    case 8: g1_body<8, CB, false, R, D>(a, sht, g, lds); break;
     }
 }
 
@@ -464,17 +471,23 @@ __global__ __launch_bounds__(64 * R) void gemv1_finish_multi_kernel(const G1Mult
 
 // ---------------------------------------------------------------- host side
 
-template <int K, int CB, int R>
+template <int K, int CB, int R, int D>
 static const void* g1_fn(bool one)
 {
-    return one ? reinterpret_cast<const void*>(&gemv1_kernel<K, CB, true, R>)
-               : reinterpret_cast<const void*>(&gemv1_kernel<K, CB, false, R>);
+    if constexpr (D > 1) {
+        static_assert(R == G1_ROWS, "deep prefetch is instantiated for the four-row template only");
+        return one ? reinterpret_cast<const void*>(&gemv1_deep_kernel<K, CB, true>)
+                   : reinterpret_cast<const void*>(&gemv1_deep_kernel<K, CB, false>);
+    } else {
+        return one ? reinterpret_cast<const void*>(&gemv1_kernel<K, CB, true, R>)
+                   : reinterpret_cast<const void*>(&gemv1_kernel<K, CB, false, R>);
+    }
 }
 
-template <int R>
+template <int R, int D = 1>
 static const void* g1_fn_kcb(int K, int cb, bool one)
 {
-#define EXL3_CASE(KK) case KK: return cb == CB_MCG ? g1_fn<KK, CB_MCG, R>(one) : g1_fn<KK, CB_3INST, R>(one);
+#define EXL3_CASE(KK) case KK: return cb == CB_MCG ? g1_fn<KK, CB_MCG, R, D>(one) : g1_fn<KK, CB_3INST, R, D>(one);
     switch (K) {
         EXL3_CASE(1) EXL3_CASE(2) EXL3_CASE(3) EXL3_CASE(4)
         EXL3_CASE(5) EXL3_CASE(6) EXL3_CASE(7) EXL3_CASE(8)
@@ -522,7 +535,10 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int 
         const char* what = "exl3_gemv (1-4 rows, split segments)";
         if (!L.multi) {
             G1Args args = *L.args;
-            const void* fn = L.R == 1 ? g1_fn_kcb<1>(L.K, L.cb, L.one) : g1_fn_kcb<G1_ROWS>(L.K, L.cb, L.one);
+            const bool deep = g1_depth(L.R, L.lds) > 1;
+            const void* fn = L.R == 1 ? g1_fn_kcb<1>(L.K, L.cb, L.one)
+                           : deep     ? g1_fn_kcb<G1_ROWS, G1_DEEP>(L.K, L.cb, L.one)
+                                      : g1_fn_kcb<G1_ROWS>(L.K, L.cb, L.one);
             int rc = g1_launch(fn, &args, L.G, L.lds, stream);
             if (rc != EXL3_OK || !L.finish) return rc;
             const void* ff = L.R == 1 ? (L.one ? reinterpret_cast<const void*>(&gemv1_finish_kernel<1, true>)
@@ -534,8 +550,11 @@ int gemv1_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int 
             return check_launch(what);
         }
         G1Multi m = *L.m;
+        const bool deep = g1_depth(L.R, L.lds) > 1;
         const void* fn = L.R == 1 ? (L.cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG, 1>)
                                                     : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST, 1>))
+                       : deep     ? (L.cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG, G1_ROWS, G1_DEEP>)
+                                                    : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST, G1_ROWS, G1_DEEP>))
                                   : (L.cb == CB_MCG ? reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_MCG, G1_ROWS>)
                                                     : reinterpret_cast<const void*>(&gemv1_multi_kernel<CB_3INST, G1_ROWS>));
         int rc = g1_launch(fn, &m, L.G, L.lds, stream);

@@ -28,8 +28,11 @@ constexpr int G1_TBATCH = 2;             // activation-table pairs a wave loads 
 // flight, and every unit more per wave lengthens the memory queues that a launch's first
 // units and activation loads wait behind: measured on MI355X (down_proj, per call), depth 1
 // against 2 and against 24 / (K + 3) clamped to 2..6: K = 2 18.6 / 18.7 / 19.6 us, K = 3
-// 18.9 / 19.6 / 20.9, K = 4 19.4 / 19.8 / 20.7, K = 5 19.4 / 20.4 / 21.4.
-constexpr int g1_depth(int) { return 1; }
+// 18.9 / 19.6 / 20.9, K = 4 19.4 / 19.8 / 20.7, K = 5 19.4 / 20.4 / 21.4.  Two for the
+// four-row template where a launch's LDS per workgroup leaves fewer than G1_WG_PER_CU
+// workgroups resident (g1_depth, after the LDS constants): fewer waves per SIMD, so each
+// keeps more bytes in flight.
+constexpr int G1_DEEP = 2;
 
 // Units per workgroup the launch aims for: fewer, longer ranges cut the cross-workgroup
 // reduction (fewer contributors per column group) and the per-wave start-up, while a
@@ -606,6 +609,17 @@ inline bool g1_any_split(const G1Group& grp)
 }
 
 constexpr size_t G1_LDS_PER_CU = 160 * 1024;
+
+// Units in flight per wave for a launch of the R-row template with `lds` bytes of LDS per
+// workgroup: 1, or G1_DEEP for the four-row template when fewer than G1_WG_PER_CU workgroups
+// fit a CU's LDS.  Measured on MI355X at settled clocks: the K = 6 lm_head (two resident) at
+// 2 / 3 / 4 rows 149 / 154 / 161 -> 136 / 151 / 155 us per call, gate_up at 4 rows (three
+// resident) 33.6-33.8 -> 32.7-33.3 us; with four resident (qkv at 4 rows) depth 2 was
+// 0.2-0.5 us slower, and at one row it did not change the lm_head.
+G1_HD int g1_depth(int R, size_t lds)
+{
+    return R > 1 && lds > G1_LDS_PER_CU / G1_WG_PER_CU ? G1_DEEP : 1;
+}
 
 // Workgroup counts G[0..ns) of one launch whose groups have U[t] units (nr activation rows in
 // the tables), for the most

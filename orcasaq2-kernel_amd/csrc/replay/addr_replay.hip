@@ -203,7 +203,8 @@ void g1_replay_wg(G1World& W, const GemvShard* shards, const G1Group& a, const G
         };
         G1Cursor pf = g1_cursor_at<K, ONE>(a, sht, w.ub + run.lo), cu = pf;
         int jpf = 0;
-        constexpr int D = g1_depth(K);
+        const int D = g1_depth(R, lds);   // the kernel's ring depth for this launch
+        if (D < 1 || D > G1_DEEP) fail("prefetch depth %d", D);
         if (n > 0) {
             check_load(pf, "first trellis load");
             for (int d = 1; d < D; d++) {
