@@ -93,8 +93,11 @@ def test_gemv1_config4_layers(rl, rows):
     ok(gemv1(rl, rows, 17408, [5120], [3]), "down_proj")
 
 
-def test_gemv1_lm_head(rl):
-    st = ok(gemv1(rl, 1, 5120, [151936], [6]), "K=6 lm_head")
+@pytest.mark.parametrize("rows", [1, 2, 4])
+def test_gemv1_lm_head(rl, rows):
+    """At 2..4 rows the launch's LDS leaves two workgroups per CU, so the kernel keeps two
+    units in flight per wave (g1_depth): the replay walks that ring too."""
+    st = ok(gemv1(rl, rows, 5120, [151936], [6]), f"K=6 lm_head rows={rows}")
     assert st[2] == 151936 // 128 * 5120 // 16
 
 
