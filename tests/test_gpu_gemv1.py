@@ -184,8 +184,9 @@ def test_gemv1_lm_head_sampled_column_groups(native, oracle):
 def test_gemv1_2_to_4_rows_on_the_lm_head(native, oracle, rows):
     """2..4 rows of the lm_head shape (5120 -> 151936, K=6): with four activation rows a
     workgroup range's tables leave fewer than three workgroups per CU resident, so the launch
-    takes G1_GMAX workgroups that run in turn; four column groups are checked against the
-    oracle on the matching trellis slice."""
+    takes G1_GMAX workgroups that run in turn, and each wave keeps two units in flight (the
+    deep four-row kernel); four column groups are checked against the oracle on the matching
+    trellis slice."""
     ic, oc, K = 5120, 151936, 6
     g = torch.Generator().manual_seed(5)
     t = syn.trellis(ic, oc, K, g)
