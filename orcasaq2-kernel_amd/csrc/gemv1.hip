@@ -123,7 +123,8 @@ __device__ __forceinline__ unsigned long long g1_fx(float v)
     return (1ull << G1_FX_CBIT) + (unsigned long long)f;
 }
 
-// Split segment S, activation row r, n contributing workgroups, accumulators in a.acc: this
+// Split segment S, activation row r, n contributing workgroups, accumulators in a.acc, sv the
+// lane's svh pair of the column group: this
 // workgroup's partial outputs (v0, v1: outputs 2 lane, 2 lane + 1 of the column group) go
 // through the output Hadamard and * svh here -- both linear, so the transformed partials of
 // the n workgroups add up to the finished outputs -- and are added into the segment's words.
@@ -135,13 +136,12 @@ __device__ __forceinline__ unsigned long long g1_fx(float v)
 // call's adds.
 template <bool ONE>
 __device__ __forceinline__ void g1_acc_add(const G1Group& a, const G1Shard* sht, int S, int R, int r, int n,
-                                           float v0, float v1, int lane)
+                                           float v0, float v1, int lane, uint32_t sv)
 {
     const int s = g1_shard_of_seg<ONE>(a, sht, S);
     const G1Shard& e = g1_sh<ONE>(sht, s);
     const int cg = S - e.sbeg;
     wave_fwht128(v0, v1);
-    const uint32_t sv = reinterpret_cast<const uint32_t*>(e.svh + cg * 128)[lane];
     const unsigned long long m0 = g1_fx(v0 * g1_lo(sv)), m1 = g1_fx(v1 * g1_hi(sv));
     unsigned long long* p = a.acc + g1_acc_word(S, R, r, lane, 0);
     const unsigned long long o0 = __hip_atomic_fetch_add(p, m0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -272,6 +272,14 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
 #pragma unroll
         for (int d = 1; d < D; d++) load(ring[d], next_pf());
     }
+    // The svh pair of this wave's first epilogue task (segment, row) = task `wave`, loaded now
+    // so that its latency is not at the end of the launch.
+    auto svh_of = [&](int t) -> uint32_t {
+        const int S = w.S_first + (R == 1 ? t : t / nr);
+        const G1Shard& e = sh(g1_shard_of_seg<ONE>(a, sht, S));
+        return reinterpret_cast<const uint32_t*>(e.svh + (S - e.sbeg) * 128)[lane];
+    };
+    const uint32_t sv_first = wave < w.nseg * nr ? svh_of(wave) : 0u;
     __syncthreads();
 
     // ---- main loop.  Scalar bookkeeping (cursor steps, column-group crossings, flushes of a
@@ -330,12 +338,11 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
     __syncthreads();
 
     // ---- per segment: fixed-order sum of the waves; finish here, or via the slots
-    auto finish = [&](int k, int r, float v0, float v1) {
+    auto finish = [&](int k, int r, float v0, float v1, uint32_t sv) {
         const int S = w.S_first + k;
         const int s = g1_shard_of_seg<ONE>(a, sht, S);
         const int cg = S - sh(s).sbeg;
         wave_fwht128(v0, v1);
-        const uint32_t sv = reinterpret_cast<const uint32_t*>(sh(s).svh + cg * 128)[lane];
         v0 *= g1_lo(sv);
         v1 *= g1_hi(sv);
         const uint32_t out = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v0) |
@@ -356,10 +363,11 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
             v0 += p.x;
             v1 += p.y;
         }
+        const uint32_t sv = t == wave ? sv_first : svh_of(t);
         int g_lo, g_hi;
         g1_contributors<ONE>(a, sht, w.S_first + k, g_lo, g_hi);
         if (g_hi > g_lo && a.acc) {
-            g1_acc_add<ONE>(a, sht, w.S_first + k, R, r, g_hi - g_lo + 1, v0, v1, lane);
+            g1_acc_add<ONE>(a, sht, w.S_first + k, R, r, g_hi - g_lo + 1, v0, v1, lane, sv);
         } else if (g_hi > g_lo) {
             // split segment without accumulators: row r of slot (S, g) holds this workgroup's 128
             // partials, which gemv1_finish_kernel adds after the launch
@@ -367,7 +375,7 @@ __device__ __forceinline__ void g1_body(const G1Group& a, const G1Shard* sht, co
             my[g1_slot_word(0, R, r)] = (uint64_t)__builtin_bit_cast(uint32_t, v0) |
                                         ((uint64_t)__builtin_bit_cast(uint32_t, v1) << 32);
         } else {
-            finish(k, r, v0, v1);
+            finish(k, r, v0, v1, sv);
         }
     }
 }
