@@ -84,8 +84,10 @@ def gpu_bench(args) -> dict:
     """Config 1 on the GPU.  Each step is captured once into a HIP graph (the way decode
     serving replays its steps) so host launch overhead is outside the measurement: W
     warm-up steps are one graph replay, the K timed steps another, bracketed by
-    synchronisation.  Per-K figures come from one graph per K, timed with HIP events on
-    the capture stream."""
+    synchronisation.  Per-K figures come from one graph per K (the K timed steps' calls of
+    that K), replayed PER_K_REPS times back to back between HIP events on the capture stream,
+    so the one launch of a graph from the host is spread over that many replays instead of
+    weighing on one replay's calls."""
     import torch
     from orcasaq2 import _native
     from orcasaq2 import synthetic as syn
@@ -153,10 +155,11 @@ def gpu_bench(args) -> dict:
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(side)
         with torch.cuda.stream(side):
-            gk.replay()
+            for _ in range(PER_K_REPS):
+                gk.replay()
         e1.record(side)
         torch.cuda.synchronize()
-        mean = e0.elapsed_time(e1) * 1e-3 / args.steps
+        mean = e0.elapsed_time(e1) * 1e-3 / (args.steps * PER_K_REPS)
         nbytes = syn.packed_bytes(ic, oc, K)
         per_k[K] = dict(bytes=nbytes, mean_us=mean * 1e6, gbs=nbytes / mean / 1e9,
                         frac=nbytes / mean / 1e9 / HBM_PEAK_GBS, total_s=mean * args.steps)
@@ -193,7 +196,8 @@ def _graph(dev, fn, settle=True):
     return graph, side
 
 
-SETTLE_S = 0.25   # seconds of sustained GPU work before any timed region
+SETTLE_S = 0.25     # seconds of sustained GPU work before any timed region
+PER_K_REPS = 5      # back-to-back replays of each per-K graph between its HIP events
 
 
 def _settle(replay, side, seconds: float = SETTLE_S) -> None:
