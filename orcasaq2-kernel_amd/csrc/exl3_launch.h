@@ -23,8 +23,10 @@ int device_cus();
 
 int reconstruct_dispatch(uint16_t* W, const uint32_t* trellis, int ic, int oc, int K, int cb, bool transposed,
                          hipStream_t stream);
+// zero / nzero: 32-bit words the first workgroup sets to 0 (a following launch's counters:
+// one launch fewer than a fill kernel of their own), or none.
 int had_dispatch(const uint16_t* in, uint16_t* out, const uint16_t* pre, const uint16_t* post,
-                 float scale, long rows, int cols, hipStream_t stream);
+                 float scale, long rows, int cols, hipStream_t stream, uint32_t* zero = nullptr, int nzero = 0);
 
 struct GemvShard {
     const uint32_t* trellis;
@@ -61,8 +63,10 @@ size_t gemm_grouped_shard_bytes(int rows, int ic, int oc);
 int gemm_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws,
                           size_t ws_bytes, hipStream_t stream, const char* what = "exl3_gemm_grouped");
 int gemm_sk_cus();
+// clear: the launch clears its tile counters first (false: the caller's previous launch on the
+// stream left them 0 -- the first sk_ntiles(rows, oc) words of ws).
 int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
-                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream);
+                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream, bool clear = true);
 int embed_dispatch(const int8_t* table, const void* scales, int scale_dtype, const int64_t* ids,
                    void* out, long n_ids, int vocab, int dim, hipStream_t stream);
 

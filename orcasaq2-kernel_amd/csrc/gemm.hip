@@ -11,7 +11,8 @@
 // set-up kernel does the Hadamard pass and clears the tile counters, one launch fewer
 // (measured on MI355X on the 27B shapes: 1-3 us faster per call at 17..144 rows, even at 384,
 // slower from 1024 rows, where the 16-byte-lane Hadamard kernel moves the larger
-// activations faster).  Above it: had_r_128, the counter clear, the stream-K kernel.
+// activations faster).  Above it: had_r_128 (whose first workgroup also clears the stream-K
+// launch's tile counters: one launch fewer, 2-4 us per call) and the stream-K kernel.
 #include "exl3_common.h"
 #include "exl3_launch.h"
 #include "gemm_sk_plan.h"
@@ -37,11 +38,12 @@ int gemm_dispatch(const uint16_t* A, const uint32_t* trellis, uint16_t* C, const
         return gemm_grouped_dispatch(A, &d, 1, rows, static_cast<char*>(workspace), ws_bytes, stream, "exl3_gemm");
     }
     uint16_t* Ah = static_cast<uint16_t*>(workspace);
-    int rc = had_dispatch(A, Ah, suh, nullptr, 1.0f, rows, ic, stream);
-    if (rc != EXL3_OK) return rc;
     const size_t ah = gemm_sk_ah_bytes(rows, ic);
-    return gemm_sk_dispatch(Ah, trellis, C, svh, static_cast<char*>(workspace) + ah, ws_bytes - ah, rows, ic, oc, K,
-                            cb, stream);
+    char* const sk_ws = static_cast<char*>(workspace) + ah;   // tile counters first, then slots
+    int rc = had_dispatch(A, Ah, suh, nullptr, 1.0f, rows, ic, stream, reinterpret_cast<uint32_t*>(sk_ws),
+                          sk_ntiles(rows, oc));
+    if (rc != EXL3_OK) return rc;
+    return gemm_sk_dispatch(Ah, trellis, C, svh, sk_ws, ws_bytes - ah, rows, ic, oc, K, cb, stream, false);
 }
 
 }  // namespace exl3

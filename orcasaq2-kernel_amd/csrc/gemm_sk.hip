@@ -797,10 +797,10 @@ static int sk_emit(const SkLaunch& L, const char* what, hipStream_t stream)
 }
 
 int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
-                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream)
+                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream, bool clear)
 {
     return sk_plan_single(Ah, trellis, C, svh, ws, ws_bytes, rows, ic, oc, K, cb, gemm_sk_cus(),
-                          [&](const SkLaunch& L) { return sk_emit(L, "exl3_gemm (stream-K)", stream); });
+                          [&](const SkLaunch& L) { return sk_emit(L, "exl3_gemm (stream-K)", stream); }, clear);
 }
 
 template <int BM>

@@ -368,10 +368,19 @@ inline int sk_place(SkArgs& a, int gmax, char* ws, size_t ws_bytes, const char* 
     return EXL3_OK;
 }
 
-// exl3_gemm's stream-K launch over one shard (Ah already transformed).
+// Tiles of exl3_gemm's single-shard launch: its tile counters are the first this many
+// 32-bit words of the launch's workspace.
+inline int sk_ntiles(int rows, int oc)
+{
+    const int bm = gemm_sk_bm(rows);
+    return ((rows + bm - 1) / bm) * sk_ntn(oc);
+}
+
+// exl3_gemm's stream-K launch over one shard (Ah already transformed); clear: the launch
+// clears its tile counters first (false: they are 0 already).
 template <class Emit>
 int sk_plan_single(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
-                   size_t ws_bytes, int rows, int ic, int oc, int K, int cb, int cus, Emit&& emit)
+                   size_t ws_bytes, int rows, int ic, int oc, int K, int cb, int cus, Emit&& emit, bool clear = true)
 {
     SkArgs a = {};
     a.rows = rows;
@@ -389,12 +398,12 @@ int sk_plan_single(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, con
     s.tbeg = 0;
     s.K = K;
     const int bm = gemm_sk_bm(rows);
-    a.ntiles = ((rows + bm - 1) / bm) * s.ntn;
+    a.ntiles = sk_ntiles(rows, oc);
     SkLaunch L = {};
     L.BM = bm;
     L.K = K;
     L.cb = cb;
-    L.clear = true;
+    L.clear = clear;
     L.args = &a;
     const char* what = "exl3_gemm (stream-K)";
     int rc;

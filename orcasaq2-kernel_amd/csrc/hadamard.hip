@@ -54,10 +54,18 @@ __device__ __forceinline__ void had_lane_stage(float (&v)[8], int lane)
     for (int i = 0; i < 8; i++) v[i] = __builtin_fmaf(v[i], sg, had_xor<D>(v[i]));
 }
 
+// Words zero[0 .. nzero) to 0 by workgroup 0 (before any of its lanes leaves).
+__device__ __forceinline__ void had_zero(uint32_t* zero, int nzero)
+{
+    if (blockIdx.x == 0)
+        for (int i = threadIdx.x; i < nzero; i += blockDim.x) zero[i] = 0u;
+}
+
 __global__ __launch_bounds__(64 * HAD_WAVES) void had_r_128_kernel(
     const uint4* in, uint4* out, const uint4* __restrict__ pre,  // in == out allowed
-    const uint4* __restrict__ post, float scale, long blocks, int blocks_per_row)
+    const uint4* __restrict__ post, float scale, long blocks, int blocks_per_row, uint32_t* zero, int nzero)
 {
+    had_zero(zero, nzero);
     const long blk = ((long)blockIdx.x * HAD_WAVES + (threadIdx.x >> 6)) * 4 + ((threadIdx.x >> 4) & 3);
     if (blk >= blocks) return;  // no barriers or cross-row exchanges leave a 16-lane row
     const int lane = threadIdx.x & 15;
@@ -105,8 +113,9 @@ __global__ __launch_bounds__(64 * HAD_WAVES) void had_r_128_kernel(
 // Pointers only 4-byte aligned: one wave per 128-block, lane l holds elements 2l, 2l + 1.
 __global__ __launch_bounds__(64 * HAD_WAVES) void had_r_128_narrow_kernel(
     const uint32_t* in, uint32_t* out, const uint32_t* __restrict__ pre,  // in == out allowed
-    const uint32_t* __restrict__ post, float scale, long blocks, int blocks_per_row)
+    const uint32_t* __restrict__ post, float scale, long blocks, int blocks_per_row, uint32_t* zero, int nzero)
 {
+    had_zero(zero, nzero);
     const long blk = (long)blockIdx.x * HAD_WAVES + (threadIdx.x >> 6);
     if (blk >= blocks) return;  // no barriers in this kernel
     const int lane = threadIdx.x & 63;
@@ -133,25 +142,25 @@ __global__ __launch_bounds__(64 * HAD_WAVES) void had_r_128_narrow_kernel(
 }
 
 int had_dispatch(const uint16_t* in, uint16_t* out, const uint16_t* pre, const uint16_t* post,
-                 float scale, long rows, int cols, hipStream_t stream)
+                 float scale, long rows, int cols, hipStream_t stream, uint32_t* zero, int nzero)
 {
     const int bpr = cols / 128;
     const long blocks = rows * bpr;
-    if (blocks == 0) return EXL3_OK;
+    if (blocks == 0 && nzero == 0) return EXL3_OK;   // with words to clear: one workgroup, no blocks
     auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
     if (!a16(in) || !a16(out) || (pre && !a16(pre)) || (post && !a16(post))) {
-        const long grid = (blocks + HAD_WAVES - 1) / HAD_WAVES;
+        const long grid = std::max<long>(1, (blocks + HAD_WAVES - 1) / HAD_WAVES);
         hipLaunchKernelGGL(had_r_128_narrow_kernel, dim3((unsigned)grid), dim3(64 * HAD_WAVES), 0, stream,
                            reinterpret_cast<const uint32_t*>(in), reinterpret_cast<uint32_t*>(out),
                            reinterpret_cast<const uint32_t*>(pre), reinterpret_cast<const uint32_t*>(post),
-                           scale, blocks, bpr);
+                           scale, blocks, bpr, zero, nzero);
         return check_launch("exl3_had_r_128");
     }
-    const long grid = (blocks + 4 * HAD_WAVES - 1) / (4 * HAD_WAVES);
+    const long grid = std::max<long>(1, (blocks + 4 * HAD_WAVES - 1) / (4 * HAD_WAVES));
     hipLaunchKernelGGL(had_r_128_kernel, dim3((unsigned)grid), dim3(64 * HAD_WAVES), 0, stream,
                        reinterpret_cast<const uint4*>(in), reinterpret_cast<uint4*>(out),
                        reinterpret_cast<const uint4*>(pre), reinterpret_cast<const uint4*>(post),
-                       scale, blocks, bpr);
+                       scale, blocks, bpr, zero, nzero);
     return check_launch("exl3_had_r_128");
 }
 

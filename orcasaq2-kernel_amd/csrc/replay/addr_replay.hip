@@ -1253,8 +1253,17 @@ int exl3r_gemm_sk(int mode, int rows, int ic, int nshards, const int* oc, const 
         };
         int rc;
         if (mode == 0) {
+            // above SK_PREP_MAX_ROWS exl3_gemm's Hadamard pass zeroes the launch's counters
+            // instead of a clear kernel: sk_ntiles words at the start of its workspace
+            auto emit_single = [&](const SkLaunch& L) {
+                if (reinterpret_cast<const char*>(L.args->counters) != fake_ptr<char>(B_WS) ||
+                    L.args->ntiles != sk_ntiles(rows, oc[0]))
+                    fail("tile counters (%d) are not the %d words the Hadamard pass clears", L.args->ntiles,
+                         sk_ntiles(rows, oc[0]));
+                return emit(L);
+            };
             rc = sk_plan_single(fake_ptr<uint16_t>(B_AH), shards[0].trellis, shards[0].C, shards[0].svh, fake_ptr<char>(B_WS),
-                                ws, rows, ic, oc[0], K[0], cb[0], cus, emit);
+                                ws, rows, ic, oc[0], K[0], cb[0], cus, emit_single, false);
         } else {
             const char* what = "exl3_gemm_grouped";
             switch (bm) {
