@@ -44,7 +44,7 @@ from . import _native
 # reference.
 GEMM_MAX_ROWS = int(os.environ.get("ORCA_EXL3_GEMM_MAX_ROWS", "144"))
 GEMM_MAX_ROWS_SET = "ORCA_EXL3_GEMM_MAX_ROWS" in os.environ
-WIDE_FUSED_MAX_ROWS = 1536           # 8192+ inputs: fused up to here
+WIDE_FUSED_MAX_ROWS = 2560           # 8192+ inputs: fused up to here
 WIDE_OUT_FUSED_ROWS = (1536, 3072)   # 4096..8191 inputs, oc >= 2 ic: fused in (lo, hi] too
 GEMV_MAX_ROWS = _native.GEMV_MAX_ROWS
 
@@ -62,12 +62,14 @@ def _fused_gemm_faster(rows: int, ic: int, oc: int) -> bool:
     GEMV_MAX_ROWS rows.  Measured on MI355X at settled clocks (us per call, HIP graph, fused /
     reconstruct branch; the branch's library GEMM is far from monotone in the row count):
       17408 -> 5120:  144: 116 / 176, 256: 118 / 225, 1024: 221 / 308, 1536: 308 / 430,
-                      2048: 397 / 373, 2560: 499 / 652, 3072: 589 / 487, 4096: 732 / 701;
+                      2048: 388 / 370, 2560: 499 / 652, 3072: 589 / 487, 4096: 732 / 701;
       5120 -> 17408:  64: 60 / 77, 128: 80 / 83, 144: 112 / 95, 384: 143 / 120,
                       1024: 220 / 232, 1536: 300 / 285, 2048: 390 / 478, 2560: 478 / 569,
                       3072: 592 / 644, 4096: 742 / 685;
       5120 -> 6144:   40: 39 / 45, 64: 46 / 46, 80: 60 / 49, 144: 71 / 52, 2048: 166 / 142.
-    So: 8192+ inputs fused up to WIDE_FUSED_MAX_ROWS (the lone win at 2560 is not taken);
+    So: 8192+ inputs fused up to WIDE_FUSED_MAX_ROWS -- at 2048 rows too, 5% slower than the
+    reconstruct branch but with no dense W_q (the branch writes and reads a 2 ic oc-byte
+    transient, 178 MB for down_proj) and no library GEMM;
     4096..8191 inputs fused up to 64 rows, and with oc >= 2 ic up to 128 rows and within
     WIDE_OUT_FUSED_ROWS; narrower inputs (unmeasured below 4096) fused up to GEMM_MAX_ROWS."""
     if ic >= 8192:
@@ -101,9 +103,14 @@ def _shard_gemm_impl(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, oc: i
         return _native.gemv(x, trellis, suh, svh, k, cb)
     if _fused_route(rows, ic, oc):
         return _native.gemm(x, trellis, suh, svh, k, cb)
-    # reconstruct branch: dense W_q lives only for the duration of the call, decoded as
-    # W_q^T (oc, ic) so the library runs its transposed-B GEMM (measured 15-20% faster than
-    # x @ W_q at 512-4096 rows on MI355X)
+    return _reconstruct_branch(x, trellis, suh, svh, k, cb)
+
+
+def _reconstruct_branch(x: Tensor, trellis: Tensor, suh: Tensor, svh: Tensor, k, cb: int) -> Tensor:
+    """The reference's prefill branch (orcasaq2/ops.py:50-59): had_r_128, reconstruct, a dense
+    GEMM, had_r_128.  The dense W_q lives only for the duration of the call, decoded as W_q^T
+    (oc, ic) so the library runs its transposed-B GEMM (measured 15-20% faster than x @ W_q at
+    512-4096 rows on MI355X)."""
     xh = _native.had_r_128(x, pre=suh)
     wt = _native.reconstruct_t(trellis, k, cb)
     y = torch.nn.functional.linear(xh, wt)

@@ -66,12 +66,12 @@ def test_shard_gemm_routing_by_shape(native, oracle, rows, oc):
     assert oracle.rel_err_rows(y.cpu().numpy(), ref(oracle, x, lin)).max() <= 1e-3
 
 
-@pytest.mark.parametrize("rows", [512, 2048])
+@pytest.mark.parametrize("rows", [512, 2048, 3072])
 def test_shard_gemm_down_proj_prefill_op_route(native, oracle, rows):
-    """The op on config 3's shape, down_proj 17408 -> 5120 at K=4, at 512 rows (above
-    GEMM_MAX_ROWS: the fused GEMM, which measured faster there for wide inputs) and 2048 rows
-    (the reconstruct branch, faster at that size): whichever route the op takes, sampled rows
-    match the oracle."""
+    """The op on config 3's shape, down_proj 17408 -> 5120 at K=4, at 512 and 2048 rows
+    (above GEMM_MAX_ROWS: the fused GEMM for wide inputs) and 3072 rows (the reconstruct
+    branch, measured faster there): whichever route the op takes, sampled rows match the
+    oracle."""
     lin = syn.linear(17408, 5120, 4, seed=3)
     x = syn.activations(rows, 17408, torch.Generator().manual_seed(rows + 33))
     d = on(lin)

@@ -311,12 +311,13 @@ def test_fused_gemm_routing_follows_the_measured_crossovers():
     assert f(64, 5120, 6144) and not f(80, 5120, 6144) and not f(144, 5120, 6144)   # q / o-like
     assert f(128, 5120, 17408) and not f(144, 5120, 17408)                           # gate / up
     assert f(144, 512, 256) and f(144, 2048, 1024)     # unmeasured narrow inputs keep the fused path
-    # above GEMM_MAX_ROWS: wide inputs (down_proj) fused to 1536 rows; gate/up-like shapes
-    # fused in (1536, 3072]; q/o-like shapes and narrow inputs reconstruct
+    # above GEMM_MAX_ROWS: wide inputs (down_proj) fused to 2560 rows (config 3's 2048
+    # included); gate/up-like shapes fused in (1536, 3072]; q/o-like shapes and narrow inputs
+    # reconstruct
     r = ops._fused_route
     if not ops.GEMM_MAX_ROWS_SET:
-        assert r(145, 17408, 5120) and r(512, 17408, 5120) and r(1536, 17408, 5120)
-        assert not r(1537, 17408, 5120) and not r(2048, 17408, 5120) and not r(4096, 17408, 5120)
+        assert r(145, 17408, 5120) and r(512, 17408, 5120) and r(2048, 17408, 5120) and r(2560, 17408, 5120)
+        assert not r(2561, 17408, 5120) and not r(3072, 17408, 5120) and not r(4096, 17408, 5120)
         assert r(2048, 5120, 17408) and r(3072, 5120, 17408)
         assert not r(1536, 5120, 17408) and not r(3073, 5120, 17408) and not r(4096, 5120, 17408)
     assert not r(145, 5120, 17408) and not r(1024, 5120, 17408)
