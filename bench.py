@@ -255,10 +255,10 @@ def prefill_bench(reps: int) -> dict:
         graph, side = _graph(dev, fn)
         return round(_time_graph(graph, side, reps) * 1e6, 1)
 
+    import orcasaq2.ops as ops
+
     def recon(x, d):
-        xh = _native.had_r_128(x, pre=d["suh"])
-        y = torch.nn.functional.linear(xh, _native.reconstruct_t(d["trellis"], d["K"], 0))
-        return _native.had_r_128(y, out=y, post=d["svh"])
+        return ops._reconstruct_branch(x, d["trellis"], d["suh"], d["svh"], d["K"], 0)
 
     out = {"single": {}, "grouped": {}}
     for name, ic, oc, K in (("down 17408->5120 K4", 17408, 5120, 4), ("gate 5120->17408 K3", 5120, 17408, 3),
