@@ -63,10 +63,10 @@ size_t gemm_grouped_shard_bytes(int rows, int ic, int oc);
 int gemm_grouped_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int rows, char* ws,
                           size_t ws_bytes, hipStream_t stream, const char* what = "exl3_gemm_grouped");
 int gemm_sk_cus();
-// clear: the launch clears its tile counters first (false: the caller's previous launch on the
-// stream left them 0 -- the first sk_ntiles(rows, oc) words of ws).
+// The launch's tile counters, the first sk_ntiles(rows, oc) words of ws, must be 0 when it
+// starts (exl3_gemm's Hadamard pass clears them).
 int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
-                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream, bool clear = true);
+                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream);
 int embed_dispatch(const int8_t* table, const void* scales, int scale_dtype, const int64_t* ids,
                    void* out, long n_ids, int vocab, int dim, hipStream_t stream);
 

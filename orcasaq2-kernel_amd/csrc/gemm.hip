@@ -43,7 +43,7 @@ int gemm_dispatch(const uint16_t* A, const uint32_t* trellis, uint16_t* C, const
     int rc = had_dispatch(A, Ah, suh, nullptr, 1.0f, rows, ic, stream, reinterpret_cast<uint32_t*>(sk_ws),
                           sk_ntiles(rows, oc));
     if (rc != EXL3_OK) return rc;
-    return gemm_sk_dispatch(Ah, trellis, C, svh, sk_ws, ws_bytes - ah, rows, ic, oc, K, cb, stream, false);
+    return gemm_sk_dispatch(Ah, trellis, C, svh, sk_ws, ws_bytes - ah, rows, ic, oc, K, cb, stream);
 }
 
 }  // namespace exl3

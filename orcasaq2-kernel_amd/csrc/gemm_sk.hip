@@ -32,12 +32,6 @@
 
 namespace exl3 {
 
-__global__ void sk_clear_kernel(uint32_t* counters, int n)
-{
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) counters[i] = 0u;
-}
-
 // Set-up of a grouped launch (SkPrepArgs): the tile counters to zero and, for every shard,
 // its activations Ah = fp16(H128(A * suh)), one wave per (shard, row, 128-input block).
 __global__ __launch_bounds__(256) void sk_prep_kernel(const SkPrepArgs a)
@@ -774,11 +768,6 @@ static int sk_lds_any(int BM)
 static int sk_emit(const SkLaunch& L, const char* what, hipStream_t stream)
 {
     SkArgs a = *L.args;
-    if (L.clear) {
-        hipLaunchKernelGGL(sk_clear_kernel, dim3((a.ntiles + 255) / 256), dim3(256), 0, stream, a.counters, a.ntiles);
-        const int rc = check_launch(what);
-        if (rc != EXL3_OK) return rc;
-    }
     if (L.prep) {
         hipLaunchKernelGGL(sk_prep_kernel, dim3((unsigned)((L.prep_waves + 3) / 4)), dim3(256), 0, stream, *L.prep_args);
         const int rc = check_launch(what);
@@ -797,10 +786,10 @@ static int sk_emit(const SkLaunch& L, const char* what, hipStream_t stream)
 }
 
 int gemm_sk_dispatch(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
-                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream, bool clear)
+                     size_t ws_bytes, int rows, int ic, int oc, int K, int cb, hipStream_t stream)
 {
     return sk_plan_single(Ah, trellis, C, svh, ws, ws_bytes, rows, ic, oc, K, cb, gemm_sk_cus(),
-                          [&](const SkLaunch& L) { return sk_emit(L, "exl3_gemm (stream-K)", stream); }, clear);
+                          [&](const SkLaunch& L) { return sk_emit(L, "exl3_gemm (stream-K)", stream); });
 }
 
 template <int BM>

@@ -276,8 +276,8 @@ template <int BM>
 inline size_t sk_ws(long tiles, int G) { return sk_align((size_t)tiles * 4) + (size_t)(tiles + G) * sk_slot_bytes<BM>(); }
 
 // exl3_gemm up to this many rows runs as the one-shard grouped launch (its set-up kernel does
-// the Hadamard pass and the counter clear in one launch); above, a Hadamard pass of its own,
-// the counter clear and the stream-K kernel.  The workspace layout is the same.
+// the Hadamard pass and the counter clear in one launch); above, a Hadamard pass of its own
+// that also clears the counters, then the stream-K kernel.  The workspace layout is the same.
 constexpr int SK_PREP_MAX_ROWS = 384;
 
 // Tile height of a prefill launch of `rows` rows.  Each weight is decoded once per row tile;
@@ -340,7 +340,6 @@ constexpr bool sk_has_k0() { return BM <= 128; }
 // One stream-K launch of the plan.
 struct SkLaunch {
     int BM, K, cb, G;            // K = 0: each tile piece takes its shard's K
-    bool clear;                  // clear the tile counters with a fill kernel first
     bool prep;                   // the set-up kernel (prep) runs first
     long prep_waves;
     const SkArgs* args;
@@ -376,11 +375,11 @@ inline int sk_ntiles(int rows, int oc)
     return ((rows + bm - 1) / bm) * sk_ntn(oc);
 }
 
-// exl3_gemm's stream-K launch over one shard (Ah already transformed); clear: the launch
-// clears its tile counters first (false: they are 0 already).
+// exl3_gemm's stream-K launch over one shard (Ah already transformed; its tile counters
+// cleared by the same Hadamard pass).
 template <class Emit>
 int sk_plan_single(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, const uint16_t* svh, char* ws,
-                   size_t ws_bytes, int rows, int ic, int oc, int K, int cb, int cus, Emit&& emit, bool clear = true)
+                   size_t ws_bytes, int rows, int ic, int oc, int K, int cb, int cus, Emit&& emit)
 {
     SkArgs a = {};
     a.rows = rows;
@@ -403,7 +402,6 @@ int sk_plan_single(const uint16_t* Ah, const uint32_t* trellis, uint16_t* C, con
     L.BM = bm;
     L.K = K;
     L.cb = cb;
-    L.clear = clear;
     L.args = &a;
     const char* what = "exl3_gemm (stream-K)";
     int rc;

@@ -1263,7 +1263,7 @@ int exl3r_gemm_sk(int mode, int rows, int ic, int nshards, const int* oc, const 
                 return emit(L);
             };
             rc = sk_plan_single(fake_ptr<uint16_t>(B_AH), shards[0].trellis, shards[0].C, shards[0].svh, fake_ptr<char>(B_WS),
-                                ws, rows, ic, oc[0], K[0], cb[0], cus, emit_single, false);
+                                ws, rows, ic, oc[0], K[0], cb[0], cus, emit_single);
         } else {
             const char* what = "exl3_gemm_grouped";
             switch (bm) {
