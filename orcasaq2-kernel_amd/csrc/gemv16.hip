@@ -277,22 +277,44 @@ __global__ __launch_bounds__(256) void gemv16_finish_multi_kernel(const G16Multi
 
 // One wave per (shard, row, 128-input block): fp16(H128(A_r * suh_s)) into the shard's
 // fragments (lane l: inputs 2l, 2l + 1, the two halves of one word).
-__global__ __launch_bounds__(256) void gemv16_prep_kernel(const G16Prep p)
+// One workgroup per (shard, 128-input block) (g16_prep_wg): the block's 16 rows transformed
+// four per wave (the four transforms' lane exchanges in flight together) into LDS, then the
+// block's fragment area written with one 16-byte store per lane, in address order.  (One wave
+// per row and block storing 4-byte words at the fragment layout's 512-byte strides took
+// 4.1 us per qkv call.)
+__global__ __launch_bounds__(G16_PREP_LANES) void gemv16_prep_kernel(const G16Prep p)
 {
-    const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (w >= p.nsh * p.rows * p.nblk) return;   // whole waves only
-    int s, r, b;
-    g16_prep_wave(p, w, s, r, b);
-    const uint32_t xw = reinterpret_cast<const uint32_t*>(p.A + (long)r * p.ic + b * 128)[lane];
+    __shared__ uint32_t xs[16][65];           // [row][input pair], padded
+    int s, b;
+    g16_prep_wg(p, blockIdx.x, s, b);
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const uint32_t sw = reinterpret_cast<const uint32_t*>(p.suh[s] + b * 128)[lane];
-    float v0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(xw & 0xffffu)) *
-               (float)__builtin_bit_cast(_Float16, (uint16_t)(sw & 0xffffu));
-    float v1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(xw >> 16)) *
-               (float)__builtin_bit_cast(_Float16, (uint16_t)(sw >> 16));
-    wave_fwht128(v0, v1);
-    const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)v0), h1 = __builtin_bit_cast(uint16_t, (_Float16)v1);
-    reinterpret_cast<uint32_t*>(p.ah[s])[g16_ah_elem(r, b * 128 + 2 * lane) >> 1] = h0 | (h1 << 16);
+    const float s0 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sw & 0xffffu));
+    const float s1 = (float)__builtin_bit_cast(_Float16, (uint16_t)(sw >> 16));
+    float v0[4], v1[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int r = wv + 4 * j;
+        const uint32_t xw = r < p.rows ? reinterpret_cast<const uint32_t*>(p.A + (long)r * p.ic + b * 128)[lane] : 0u;
+        v0[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(xw & 0xffffu)) * s0;
+        v1[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(xw >> 16)) * s1;
+    }
+    wave_fwht128_n<4>(v0, v1, fwht_signs(lane));
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t h0 = __builtin_bit_cast(uint16_t, (_Float16)v0[j]);
+        const uint32_t h1 = __builtin_bit_cast(uint16_t, (_Float16)v1[j]);
+        xs[wv + 4 * j][lane] = h0 | (h1 << 16);
+    }
+    __syncthreads();
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        int i, k;
+        g16_prep_src(4 * threadIdx.x + e, i, k);
+        o[e] = xs[i][k >> 1];
+    }
+    reinterpret_cast<uint4*>(p.ah[s] + g16_prep_base(b))[threadIdx.x] = uint4{o[0], o[1], o[2], o[3]};
 }
 
 // ---------------------------------------------------------------- host side
@@ -336,8 +358,8 @@ int gemv16_dispatch(const uint16_t* A, const GemvShard* shards, int nshards, int
     bool prepped = false;
     return g16_plan(A, shards, nshards, rows, ws, ws_bytes, device_cus(), prep, [&](const G16Launch& L) {
         if (!prepped) {
-            const long waves = (long)prep.nsh * prep.rows * prep.nblk;
-            hipLaunchKernelGGL(gemv16_prep_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, prep);
+            hipLaunchKernelGGL(gemv16_prep_kernel, dim3((unsigned)(prep.nsh * prep.nblk)), dim3(G16_PREP_LANES), 0,
+                               stream, prep);
             const int rc = check_launch(what);
             if (rc != EXL3_OK) return rc;
             prepped = true;

@@ -196,7 +196,7 @@ G1_HD int g16_ah_word(int m, int lane)
 }
 
 // The lane whose A fragment lane l reads when the call has nrows rows: lane 16 j + i holds
-// activation row i, and a row past nrows (written by no set-up wave; its C row is never
+// activation row i, and a row past nrows (zeros from the set-up; its C row is never
 // stored) reads row nrows - 1 of the same k-group instead.
 G1_HD int g16_ah_lane(int lane, int nrows)
 {
@@ -265,8 +265,9 @@ inline size_t g16_shard_bytes(int ic, int oc)
     return ah + (size_t)(G1_GMAX + oc / G16_STRIP) * G16_ROWS * G16_STRIP * 4;
 }
 
-// Set-up kernel of a call: for every shard s, row r < nrows and 128-input block b, one wave
-// writes fp16(H128(A_r * suh_s)) of block b into the shard's fragments.
+// Set-up kernel of a call: for every shard s and 128-input block b, one workgroup writes
+// fp16(H128(A_r * suh_s)) of block b for the rows r < nrows (zeros for the others) into the
+// shard's fragments.
 struct G16Prep {
     const uint16_t* A;
     int rows, ic, nsh, nblk;
@@ -274,12 +275,27 @@ struct G16Prep {
     uint32_t* ah[EXL3_MAX_SHARDS];
 };
 
-G1_HD void g16_prep_wave(const G16Prep& p, int w, int& s, int& r, int& b)
+// Set-up workgroup g (four waves) of a call: shard s, 128-input block b.  Wave wv transforms
+// activation rows wv, wv + 4, wv + 8, wv + 12 (rows from `rows` on are zeros: no decode lane
+// reads them, g16_ah_lane), then lane t of the workgroup stores words 4 t .. 4 t + 3 of the
+// block's fragment area -- units 2 b and 2 b + 1, 2 G16_AH_UNIT words from word
+// g16_prep_base(b) of the shard's fragments -- one 16-byte store each, in lane order.
+constexpr int G16_PREP_LANES = 256;
+G1_HD void g16_prep_wg(const G16Prep& p, int g, int& s, int& b)
 {
-    b = w % p.nblk;
-    const int rs = w / p.nblk;
-    r = rs % p.rows;
-    s = rs / p.rows;
+    b = g % p.nblk;
+    s = g / p.nblk;
+}
+G1_HD long g16_prep_base(int b) { return (long)b * 2 * G16_AH_UNIT; }
+// Activation row i and input k (of the block's 128; k even) of the two inputs in word w of a
+// block's fragment area: word (m 64 + 16 j + i) 2 + h of unit qq holds inputs
+// 64 qq + 16 j + 8 h + 2 m and the next (g16_ah_elem).
+G1_HD void g16_prep_src(int w, int& i, int& k)
+{
+    const int qq = w / G16_AH_UNIT, ww = w % G16_AH_UNIT;
+    const int m = ww >> 7, lf = (ww >> 1) & 63, h = ww & 1;
+    i = lf & 15;
+    k = 64 * qq + 16 * (lf >> 4) + 8 * h + 2 * m;
 }
 
 struct G16Launch {

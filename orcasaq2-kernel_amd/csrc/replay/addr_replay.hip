@@ -962,24 +962,36 @@ int g16_shard_index(const G16World& W, const GemvShard* shards, const uint32_t* 
 
 void g16_replay_prep(G16World& W, const G16Prep& p)
 {
-    const long waves = 4 * (((long)p.nsh * p.rows * p.nblk + 3) / 4);
-    for (long w = 0; w < waves; w++) {
-        if (w >= (long)p.nsh * p.rows * p.nblk) continue;
-        int s, r, b;
-        g16_prep_wave(p, (int)w, s, r, b);
-        if (s >= p.nsh || r >= p.rows || b >= p.nblk) fail("set-up wave %ld -> (%d, %d, %d)", w, s, r, b);
-        const long words = g16_ah_words(p.ic);
+    const long words = g16_ah_words(p.ic);
+    for (long g = 0; g < (long)p.nsh * p.nblk; g++) {
+        int s, b;
+        g16_prep_wg(p, (int)g, s, b);
+        if (s < 0 || s >= p.nsh || b < 0 || b >= p.nblk) fail("set-up workgroup %ld -> (%d, %d)", g, s, b);
         if (buf_of(p.ah[s]) != B_WS || off_of(p.ah[s]) != W.ah_off[s]) fail("fragments of shard %d misplaced", s);
+        if (W.ah_off[s] % 16) fail("fragments of shard %d not 16-byte aligned", s);
         if (W.ah_off[s] + words * 4 > (long)W.ws_bytes) fail("fragments of shard %d beyond the workspace", s);
-        for (int lane = 0; lane < 64; lane++) {
-            need_in(reinterpret_cast<const uint32_t*>(p.A + (long)r * p.ic + b * 128) + lane, 4, B_X, (long)W.rows * W.ic * 2, "A load (set-up)");
+        for (int t = 0; t < G16_PREP_LANES; t++) {
+            const int wv = t >> 6, lane = t & 63;
+            for (int j = 0; j < 4; j++)   // rows wv + 4 j below rows are loaded
+                if (wv + 4 * j < p.rows)
+                    need_in(reinterpret_cast<const uint32_t*>(p.A + (long)(wv + 4 * j) * p.ic + b * 128) + lane, 4, B_X,
+                            (long)W.rows * W.ic * 2, "A load (set-up)");
             need_in(reinterpret_cast<const uint32_t*>(p.suh[s] + b * 128) + lane, 4, B_SUH + s, (long)W.ic * 2, "suh load (set-up)");
-            // inputs 2 lane and 2 lane + 1 of the block: the two halves of one word
-            const long e = g16_ah_elem(r, b * 128 + 2 * lane);
-            if (e < 0 || e + 2 > 2 * words || (e & 1)) fail("fragment store at half %ld of %ld", e, 2 * words);
-            if (g16_ah_elem(r, b * 128 + 2 * lane + 1) != e + 1) fail("fragment inputs %d, %d not one word", b * 128 + 2 * lane, b * 128 + 2 * lane + 1);
-            if (W.ah_written[s][e >> 1]) fail("fragment word %ld of shard %d written twice", e >> 1, s);
-            W.ah_written[s][e >> 1] = 1;
+            // the lane's 16-byte store: words 4 t .. 4 t + 3 of the block's area, each the two
+            // inputs g16_prep_src names, at the word where the decode's reads look for them
+            const long w0 = g16_prep_base(b) + 4 * t;
+            if (w0 < 0 || w0 + 4 > words) fail("fragment store at word %ld of %ld", w0, words);
+            for (int e = 0; e < 4; e++) {
+                int i, k;
+                g16_prep_src(4 * t + e, i, k);
+                if (i < 0 || i >= 16 || k < 0 || k + 1 >= 128 || (k & 1)) fail("set-up word %d -> row %d input %d", 4 * t + e, i, k);
+                const long el = g16_ah_elem(i, b * 128 + k);
+                if (el != 2 * (w0 + e) || g16_ah_elem(i, b * 128 + k + 1) != el + 1)
+                    fail("set-up word %ld holds row %d inputs %d, %d, which the reads look for at half %ld", w0 + e, i,
+                         b * 128 + k, b * 128 + k + 1, el);
+                if (W.ah_written[s][w0 + e]) fail("fragment word %ld of shard %d written twice", w0 + e, s);
+                W.ah_written[s][w0 + e] = 1;
+            }
         }
     }
 }
