@@ -275,9 +275,7 @@ __global__ __launch_bounds__(256) void gemv16_finish_multi_kernel(const G16Multi
                            4 * blockIdx.y + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
 }
 
-// One wave per (shard, row, 128-input block): fp16(H128(A_r * suh_s)) into the shard's
-// fragments (lane l: inputs 2l, 2l + 1, the two halves of one word).
-// One workgroup per (shard, 128-input block) (g16_prep_wg): the block's 16 rows transformed
+// fp16(H128(A_r * suh_s)) into the shard's fragments.  One workgroup per (shard, 128-input block) (g16_prep_wg): the block's 16 rows transformed
 // four per wave (the four transforms' lane exchanges in flight together) into LDS, then the
 // block's fragment area written with one 16-byte store per lane, in address order.  (One wave
 // per row and block storing 4-byte words at the fragment layout's 512-byte strides took
