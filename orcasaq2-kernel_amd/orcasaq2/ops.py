@@ -22,10 +22,11 @@ Dispatch on the number of activation rows (reference: orcasaq2/ops.py:25, 46-59)
   * rows > GEMM_MAX_ROWS  the reference's reconstruct branch: had_r_128(x, suh), dense W_q
                           (decoded transposed, (oc, ic)) into a scratch freed on exit, library
                           fp16 transposed-B GEMM, had_r_128(y, svh) -- except, while the row
-                          knob is at its default, the shapes where the fused kernel measured
-                          faster (_fused_gemm_faster: 8192+ inputs up to WIDE_FUSED_MAX_ROWS
-                          rows, 4096..8191 inputs with at least twice as many outputs in
-                          WIDE_OUT_FUSED_ROWS); a fused layer whose shards all route fused
+                          knob is at its default, 8192+ inputs up to WIDE_FUSED_MAX_ROWS rows
+                          (faster fused but at 2048 rows, kept fused there for no dense W_q)
+                          and 4096..8191 inputs with at least twice as many outputs in
+                          WIDE_OUT_FUSED_ROWS, where the fused kernel measured faster
+                          (_fused_gemm_faster); a fused layer whose shards all route fused
                           runs them as one grouped launch (shards_gemm).
 The op is registered for the "cuda" device type (ROCm) only: there is no CPU path.
 """
